@@ -1,0 +1,245 @@
+"""Optimizer-step benchmark on one MI355X.
+
+One step is one pass of the fused hot path over a resident parameter set:
+GradScaler.unscale_ -> clip_grad_norm_(max_norm=1.0) -> GradScaler.step
+(AdamW) -> GradScaler.update, exactly the call sequence of the reference's
+training loop (train.py:483-491), driven through this package's drop-in API.
+
+Default workload: the Qwen3-8B-shaped parameter set (399 tensors,
+8,190,735,360 params), bf16 params and grads, fp32 master / exp_avg /
+exp_avg_sq (131 GB resident), synthetic data.  Prints one JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+mg = importlib.import_module("minigpt-train-infra_amd")
+syn = importlib.import_module("minigpt-train-infra_amd.synthetic")
+
+METRIC = "optimizer steps/sec + achieved HBM GB/s (% of peak) at Qwen3-8B-shaped 8.2B params"
+HBM_PEAK_GBPS = 8000.0
+# compulsory bytes per parameter of one executed step, by (param dtype, grad dtype):
+# grad read + param (or master) read/write + exp_avg read/write + exp_avg_sq read/write
+# (+ the bf16/fp16 model-copy write when a master exists)
+BYTES_PER_PARAM = {("bf16", "bf16"): 28, ("f32", "f32"): 28, ("f32", "f16"): 26, ("f16", "f16"): 28}
+DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+WORKLOADS = {
+    "qwen3_8b": dict(param="bf16", grad="bf16"),
+    "gpt_1p3b": dict(param="bf16", grad="bf16"),
+    "gpt2_small": dict(param="f32", grad="f16"),
+    "ragged_20k": dict(param="f32", grad="f16"),
+    "minigpt_tiny_cpu": dict(param="f32", grad="f32"),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_workload(name: str, dev: torch.device):
+    spec = WORKLOADS[name]
+    shapes = mg.paramsets.WORKLOADS[name]()
+    decay = [(n, s) for n, s in shapes if len(s) >= 2]
+    nodecay = [(n, s) for n, s in shapes if len(s) < 2]
+    ordered = decay + nodecay
+    params = []
+    for i, (_, s) in enumerate(ordered):
+        p = torch.empty(s, dtype=DT[spec["param"]], device=dev)
+        syn.fill_(p, syn.PARAM_SEED, syn.param_stream(i), 0.02)
+        params.append(torch.nn.Parameter(p))
+    groups = [
+        {"params": params[: len(decay)], "param_names": [n for n, _ in decay], "group_name": "decay", "weight_decay": 0.1},
+        {"params": params[len(decay):], "param_names": [n for n, _ in nodecay], "group_name": "no_decay", "weight_decay": 0.0},
+    ]
+    return spec, ordered, params, [g for g in groups if g["params"]]
+
+
+def time_cpu_baseline(name: str, budget_params: int) -> dict:
+    """The reference's CPU step (torch 2.10 on the host cores) on a bounded,
+    contiguous sample of the workload's tensors, extrapolated per parameter."""
+    from oracle.torch_path import time_reference_step
+
+    shapes = mg.paramsets.WORKLOADS[name]()
+    sample, n = [], 0
+    for _, s in shapes:
+        k = math.prod(s)
+        if n + k > budget_params and sample:
+            continue
+        sample.append(s)
+        n += k
+        if n >= budget_params:
+            break
+    total = sum(math.prod(s) for _, s in shapes)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    r = time_reference_step(sample, steps=5, scaler=True, threads=threads)
+    ns_per_param = r["seconds"] / r["params"] * 1e9
+    return {
+        "value": 1.0 / (ns_per_param * 1e-9 * total),
+        "unit": "steps/s",
+        "cores": r["threads"],
+        "kind": "reference",
+        "sample": (f"torch {torch.__version__.split('+')[0]} CPU AdamW(fused=False) + clip_grad_norm_ + "
+                   f"GradScaler('cpu'), the calls of train.py:485-491, on {r['tensors']} tensors / {r['params']:,} fp32 params "
+                   f"of the workload; median of 5 steps = {r['seconds']*1e3:.1f} ms ({ns_per_param:.3f} ns/param: "
+                   f"unscale {r['unscale_s']*1e3:.1f} ms, clip {r['clip_s']*1e3:.1f} ms, step {r['step_s']*1e3:.1f} ms, "
+                   f"update {r['update_s']*1e3:.2f} ms), extrapolated to {total:,} params"),
+    }
+
+
+def read_traffic(name: str) -> float | None:
+    """HBM bytes per pass-2 launch measured with rocprofv3 counters, when a
+    profile summary for this workload is committed under profiles/."""
+    f = ROOT / "profiles" / f"adamw_kernel_{name}_traffic.json"
+    if f.exists():
+        try:
+            return float(json.loads(f.read_text())["bytes_per_launch"])
+        except (KeyError, ValueError):
+            return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="qwen3_8b", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-params", type=int, default=600_000_000)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (use --gpus 1)", file=sys.stderr)
+        return 2
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    spec, ordered, params, groups = build_workload(args.workload, dev)
+    n_params = sum(p.numel() for p in params)
+    log(f"workload {args.workload}: {len(params)} tensors, {n_params:,} params ({spec['param']} params, {spec['grad']} grads)")
+
+    init_scale = 65536.0
+    opt = mg.AdamW(groups, lr=3e-4, betas=(0.9, 0.95), eps=1e-8)
+    scaler = mg.GradScaler("cuda", init_scale=init_scale, growth_factor=2.0, backoff_factor=0.5, growth_interval=2000)
+    scaler.scale(torch.ones((), device=dev))
+    if spec["grad"] == spec["param"]:
+        for i, p in enumerate(params):
+            p.grad = syn.fill_(torch.empty_like(p), syn.GRAD_SEED, syn.grad_stream(1, i), 1e-3 * init_scale)
+    else:
+        grads = [syn.fill_(torch.empty(p.shape, dtype=DT[spec["grad"]], device=dev), syn.GRAD_SEED,
+                           syn.grad_stream(1, i), 1e-3 * init_scale) for i, p in enumerate(params)]
+        opt.set_grad_source(grads)
+    torch.cuda.synchronize()
+    log(f"resident: {torch.cuda.memory_allocated(dev) / 1e9:.1f} GB after optimizer state allocation")
+
+    eng = opt._get_engine()
+    stream = torch.cuda.current_stream(dev)
+    ev = {"norm": [], "adamw": []}
+
+    def one_step(record: bool) -> None:
+        mg.set_optimizer_lr(opt, 3e-4)
+        scaler.unscale_(opt)
+        if record:
+            a = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+        mg.clip_grad_norm_(params, 1.0)
+        if record:
+            b = torch.cuda.Event(enable_timing=True)
+            b.record(stream)
+        scaler.step(opt)
+        if record:
+            c = torch.cuda.Event(enable_timing=True)
+            c.record(stream)
+            ev["norm"].append((a, b))
+            ev["adamw"].append((b, c))
+        scaler.update()
+
+    for _ in range(args.warmup):
+        one_step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_step(True)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    step_s = (t1 - t0) / args.steps
+    skipped = int(round(args.steps + args.warmup - float(eng.steps.max())))
+    if eng.error_flag() != 0 or skipped != 0:
+        log(f"error flag {eng.error_flag()}, skipped {skipped}")
+        return 1
+    norm_ms = sum(a.elapsed_time(b) for a, b in ev["norm"]) / len(ev["norm"])
+    adamw_ms = sum(a.elapsed_time(b) for a, b in ev["adamw"]) / len(ev["adamw"])
+
+    bpp = BYTES_PER_PARAM[(spec["param"], spec["grad"])]
+    grad_bytes = 2 if spec["grad"] != "f32" else 4
+    achieved_step = bpp * n_params / step_s / 1e9
+    adamw_gbps = bpp * n_params / (adamw_ms * 1e-3) / 1e9
+    norm_gbps = grad_bytes * n_params / (norm_ms * 1e-3) / 1e9
+    log(f"step {step_s*1e3:.3f} ms ({1/step_s:.2f} steps/s); compulsory {bpp} B/param -> {achieved_step:.0f} GB/s "
+        f"({100*achieved_step/HBM_PEAK_GBPS:.1f}% of peak); norm pass {norm_ms:.3f} ms ({norm_gbps:.0f} GB/s), "
+        f"AdamW pass {adamw_ms:.3f} ms ({adamw_gbps:.0f} GB/s)")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the reference's CPU step on a bounded sample ...")
+        cpu = time_cpu_baseline(args.workload, args.cpu_sample_params)
+        log(f"cpu baseline {cpu['value']:.5f} steps/s on {cpu['cores']} threads")
+
+    out = {
+        "metric": METRIC,
+        "value": 1.0 / step_s,
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded counter-hash generator; random-init parameters of the named shapes)",
+        "config": {
+            "workload": args.workload,
+            "tensors": len(params),
+            "params": n_params,
+            "param_dtype": spec["param"],
+            "grad_dtype": spec["grad"],
+            "state": "fp32 master/exp_avg/exp_avg_sq" if spec["param"] != "f32" else "fp32 exp_avg/exp_avg_sq",
+            "step": "GradScaler.unscale_ + clip_grad_norm_(1.0) + AdamW + GradScaler.update",
+            "parallelism": "single GPU",
+        },
+        "achieved_GBps": achieved_step,
+        "pct_of_hbm_peak": 100.0 * achieved_step / HBM_PEAK_GBPS,
+        "bytes_per_param": bpp,
+        "passes_ms": {"norm": norm_ms, "adamw": adamw_ms},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": adamw_gbps,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": adamw_gbps / HBM_PEAK_GBPS,
+            "traffic": read_traffic(args.workload),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,34 @@
+"""MI355X-native optimizer step for MiniGPT-style training.
+
+Drop-in replacements for the torch calls of the reference's training loop
+(train.py:359-370, 457-491):
+
+    AdamW            for torch.optim.AdamW
+    GradScaler       for torch.amp.GradScaler
+    clip_grad_norm_  for torch.nn.utils.clip_grad_norm_
+
+plus the loop's host helpers (build_adamw_param_groups, set_optimizer_lr,
+cosine_lr, optimizer_completed_steps).  The arithmetic runs in hand-written
+gfx950 kernels (libmgopt.so, C ABI in include/mgopt.h); there is no CPU path.
+
+The package directory name contains hyphens, so import it with
+importlib.import_module("minigpt-train-infra_amd").
+"""
+
+from .adamw import AdamW
+from .clip_grad import clip_grad_norm_
+from .grad_scaler import GradScaler, OptState
+from .schedule import build_adamw_param_groups, cosine_lr, optimizer_completed_steps, set_optimizer_lr
+from . import paramsets
+
+__all__ = [
+    "AdamW",
+    "GradScaler",
+    "OptState",
+    "clip_grad_norm_",
+    "build_adamw_param_groups",
+    "cosine_lr",
+    "set_optimizer_lr",
+    "optimizer_completed_steps",
+    "paramsets",
+]

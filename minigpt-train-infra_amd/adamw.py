@@ -1,0 +1,293 @@
+"""AdamW with the torch.optim.AdamW surface, stepped by libmgopt on one GPU.
+
+Drop-in for the optimizer the reference builds at train.py:359-365: same
+constructor arguments, param_groups (any extra keys such as param_names and
+group_name are kept), step/zero_grad, and torch-format state_dict
+({"state": {i: {"step", "exp_avg", "exp_avg_sq"}}, "param_groups": [...]},
+torch/optim/optimizer.py:677-767).
+
+Differences a caller can observe, all by design:
+  - optimizer state lives in flat device arenas; optimizer.state[p] holds
+    views into them.  Assigning new tensors into optimizer.state (as
+    src/minigpt/optim.py:242-251 does when migrating checkpoints) is picked up
+    and copied into the arenas before the next step.
+  - bf16/fp16 parameters are updated through an fp32 master copy (state key
+    "master_param"); exp_avg/exp_avg_sq are always fp32.
+  - amsgrad and differentiable are not supported (the reference uses neither).
+"""
+
+from __future__ import annotations
+
+from collections import defaultdict
+from typing import Any, Iterable
+
+import torch
+from torch.utils.weak import WeakIdKeyDictionary
+
+from .engine import _Engine
+
+#: parameter -> engine of the AdamW instance that owns it (used by clip_grad_norm_)
+_ENGINE_OF: WeakIdKeyDictionary = WeakIdKeyDictionary()
+
+
+class _TrackedState(defaultdict):
+    """optimizer.state that notices when whole entries are replaced."""
+
+    def __init__(self, owner: "AdamW"):
+        super().__init__(dict)
+        self._owner = owner
+
+    def __setitem__(self, key, value):
+        super().__setitem__(key, value)
+        self._owner._state_dirty = True
+
+    def __delitem__(self, key):
+        super().__delitem__(key)
+        self._owner._state_dirty = True
+
+    def clear(self):
+        super().clear()
+        self._owner._state_dirty = True
+
+    def update(self, *args, **kwargs):
+        super().update(*args, **kwargs)
+        self._owner._state_dirty = True
+
+    def pop(self, *args):
+        r = super().pop(*args)
+        self._owner._state_dirty = True
+        return r
+
+    def __reduce__(self):
+        return (dict, (dict(self),))
+
+
+class AdamW(torch.optim.Optimizer):
+    """torch.optim.AdamW (decoupled weight decay), executed by the fused
+    unscale + clip + AdamW kernels.  Extra keyword arguments:
+
+    master_weights: None (auto: on for bf16/fp16 params) or True.
+    writeback_grads: also store the unscaled, clipped gradient into each
+        .grad during the step (the reference leaves them in .grad;
+        train.py never reads them after the step, so this is off by default).
+    chunk_elems: elements per work-group (a multiple of 4096).
+    """
+
+    # GradScaler.step hands found_inf/grad_scale to the optimizer instead of
+    # syncing on the host (torch/amp/grad_scaler.py:403-454).
+    _step_supports_amp_scaling = True
+
+    def __init__(
+        self,
+        params: Iterable[Any],
+        lr: float = 1e-3,
+        betas: tuple[float, float] = (0.9, 0.999),
+        eps: float = 1e-8,
+        weight_decay: float = 1e-2,
+        amsgrad: bool = False,
+        *,
+        maximize: bool = False,
+        foreach: bool | None = None,
+        capturable: bool = False,
+        differentiable: bool = False,
+        fused: bool | None = None,
+        master_weights: bool | None = None,
+        writeback_grads: bool = False,
+        chunk_elems: int | None = None,
+    ):
+        if isinstance(lr, torch.Tensor) and lr.numel() != 1:
+            raise ValueError("Tensor lr must be 1-element")
+        if not 0.0 <= lr:
+            raise ValueError(f"Invalid learning rate: {lr}")
+        if not 0.0 <= eps:
+            raise ValueError(f"Invalid epsilon value: {eps}")
+        if not 0.0 <= betas[0] < 1.0:
+            raise ValueError(f"Invalid beta parameter at index 0: {betas[0]}")
+        if not 0.0 <= betas[1] < 1.0:
+            raise ValueError(f"Invalid beta parameter at index 1: {betas[1]}")
+        if not 0.0 <= weight_decay:
+            raise ValueError(f"Invalid weight_decay value: {weight_decay}")
+        if amsgrad:
+            raise NotImplementedError("amsgrad is not supported by this AdamW")
+        if differentiable:
+            raise NotImplementedError("differentiable=True is not supported by this AdamW")
+        defaults = dict(
+            lr=lr,
+            betas=betas,
+            eps=eps,
+            weight_decay=weight_decay,
+            amsgrad=amsgrad,
+            maximize=maximize,
+            foreach=foreach,
+            capturable=capturable,
+            differentiable=differentiable,
+            fused=fused,
+            decoupled_weight_decay=True,
+        )
+        super().__init__(params, defaults)
+        self._master_weights = master_weights
+        self._writeback = bool(writeback_grads)
+        self._chunk_elems = chunk_elems
+        self._engine: _Engine | None = None
+        self._state_dirty = False
+        self._installed: set[int] = set()
+        self.state = _TrackedState(self)
+        self._state_dirty = False
+
+    # ----------------------------------------------------------- internals
+    def _get_engine(self) -> _Engine:
+        if self._engine is None:
+            self._engine = _Engine(self, self._master_weights, self._chunk_elems)
+            for p in self._engine.params:
+                _ENGINE_OF[p] = self._engine
+        return self._engine
+
+    def _reconcile_state(self) -> None:
+        """Copies state entries a caller assigned directly into the arenas."""
+        eng = self._get_engine()
+        self._sync_all_masters()
+        for i, p in enumerate(eng.params):
+            entry = dict.get(self.state, p)
+            views = eng.views[i]
+            if not entry:
+                if i in self._installed:
+                    # entry removed: the parameter starts from fresh state
+                    views["exp_avg"].zero_()
+                    views["exp_avg_sq"].zero_()
+                    views["step"].zero_()
+                    self._installed.discard(i)
+                continue
+            if all(entry.get(k) is views[k] for k in ("step", "exp_avg", "exp_avg_sq")):
+                continue
+            self._copy_in(i, entry)
+        self._install_views(only_existing=True)
+        eng.t_bound = max(eng.t_bound, int(eng.steps.max().item()) if len(eng.params) else 0)
+        self._state_dirty = False
+
+    def _copy_in(self, i: int, entry: dict[str, Any]) -> None:
+        eng = self._get_engine()
+        views = eng.views[i]
+        step = entry.get("step", 0.0)
+        views["step"].fill_(float(step.item()) if isinstance(step, torch.Tensor) else float(step))
+        for key in ("exp_avg", "exp_avg_sq"):
+            src = entry.get(key)
+            if src is None:
+                views[key].zero_()
+            else:
+                if src.numel() != views[key].numel():
+                    raise ValueError(f"state {key} of parameter {i} has {src.numel()} elements, expected {views[key].numel()}")
+                views[key].copy_(src.reshape(views[key].shape))
+        if "master_param" in views and entry.get("master_param") is not None:
+            views["master_param"].copy_(entry["master_param"].reshape(views["master_param"].shape))
+        self._installed.add(i)
+
+    def _sync_all_masters(self) -> None:
+        """Master copies start from the current bf16/fp16 parameters; saved
+        masters copied in afterwards take precedence."""
+        eng = self._get_engine()
+        if not eng.has_master or eng.master_synced:
+            return
+        for i, p in enumerate(eng.params):
+            if "master_param" in eng.views[i]:
+                eng.views[i]["master_param"].copy_(p.detach())
+        eng.master_synced = True
+
+    def _install_views(self, only_existing: bool = False) -> None:
+        eng = self._get_engine()
+        for i, p in enumerate(eng.params):
+            if only_existing and i not in self._installed:
+                continue
+            dict.__setitem__(self.state, p, dict(eng.views[i]))
+            self._installed.add(i)
+
+    # ------------------------------------------------------------ surface
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        eng = self._get_engine()
+        if self._state_dirty:
+            self._reconcile_state()
+        grads = eng.current_grads()
+        eng.step(
+            found_inf=getattr(self, "found_inf", None),
+            grad_scale=getattr(self, "grad_scale", None),
+            writeback=self._writeback,
+        )
+        # torch creates state on a parameter's first step with a grad (adam.py:153-184)
+        for i, (p, g) in enumerate(zip(eng.params, grads)):
+            if g is not None and i not in self._installed:
+                dict.__setitem__(self.state, p, dict(eng.views[i]))
+                self._installed.add(i)
+        return loss
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        super().zero_grad(set_to_none=set_to_none)
+        if self._engine is not None:
+            self._engine.reset_iteration()
+
+    def set_grad_source(self, grads: Iterable[torch.Tensor | None] | None) -> None:
+        """Reads gradients from these tensors (one per parameter, in
+        param_groups order; fp32, fp16 or bf16) instead of p.grad.  None
+        restores p.grad."""
+        self._get_engine().set_grad_source(None if grads is None else list(grads))
+
+    def sync_master_from_params(self) -> None:
+        """Re-reads bf16/fp16 parameters into the fp32 master copy (after the
+        parameters were overwritten outside the optimizer)."""
+        self._get_engine().sync_master()
+
+    def add_param_group(self, param_group: dict[str, Any]) -> None:
+        if getattr(self, "_engine", None) is not None:
+            raise RuntimeError("add_param_group after the first step is not supported; build the optimizer with all groups")
+        super().add_param_group(param_group)
+
+    def state_dict(self) -> dict[str, Any]:
+        if self._state_dirty:
+            self._reconcile_state()
+        return super().state_dict()
+
+    def load_state_dict(self, state_dict: dict[str, Any]) -> None:
+        groups = self.param_groups
+        saved_groups = state_dict["param_groups"]
+        if len(groups) != len(saved_groups):
+            raise ValueError("loaded state dict has a different number of parameter groups")
+        if any(len(g["params"]) != len(s["params"]) for g, s in zip(groups, saved_groups)):
+            raise ValueError("loaded state dict contains a parameter group that doesn't match the size of optimizer's group")
+        eng = self._get_engine()
+        id_to_param = {}
+        for g, s in zip(groups, saved_groups):
+            for pid, p in zip(s["params"], g["params"]):
+                id_to_param[pid] = p
+        index = {id(p): i for i, p in enumerate(eng.params)}
+        new_groups = []
+        for g, s in zip(groups, saved_groups):
+            ng = {k: v for k, v in s.items() if k != "params"}
+            ng["params"] = g["params"]
+            if "param_names" in g and "param_names" not in ng:
+                ng["param_names"] = g["param_names"]
+            new_groups.append(ng)
+        self.param_groups = new_groups
+        # loading replaces all state: parameters absent from the saved state start fresh
+        eng.exp_avg.zero_()
+        eng.exp_avg_sq.zero_()
+        eng.steps.zero_()
+        self._installed.clear()
+        eng.master_synced = False
+        self._sync_all_masters()
+        for pid, entry in state_dict["state"].items():
+            p = id_to_param.get(pid)
+            if p is None:
+                continue
+            self._copy_in(index[id(p)], entry)
+        dict.clear(self.state)
+        self._install_views(only_existing=True)
+        eng.t_bound = int(eng.steps.max().item())
+        eng.reset_iteration()
+        self._state_dirty = False
+
+    def __setstate__(self, state: dict[str, Any]) -> None:
+        super().__setstate__(state)
+        self._engine = None

@@ -1,0 +1,967 @@
+// mgopt.hip -- fused optimizer step for one MI355X (gfx950).
+//
+// One training-loop iteration of the reference (train.py:483-491) becomes:
+//
+//   pass 1   norm_kernel       read every grad once: unscale, non-finite flag,
+//                              fp64 sum of squares -> one partial per chunk
+//   finalize finalize_kernel   one work-group: total norm, clip coefficient,
+//                              found_inf (fixed reduction order: bit-stable)
+//   prologue prologue_kernel   per-tensor step += 1 unless found_inf
+//   pass 2   adamw_kernel      read grad/param/m/v once, write param/m/v
+//                              (+ bf16/fp16 model copy): unscale, clip, AdamW
+//   update   scaler_kernel     GradScaler scale/growth-tracker state machine
+//
+// Every scalar decision (skip, scale, coefficient, step count) stays on the
+// device, so the host never waits on the GPU inside a step.
+//
+// The element arithmetic follows torch 2.10.0's CPU path (the reference's
+// pinned numerics) operation by operation; the comments on adam_elem give the
+// torch source lines.  Build with -ffp-contract=off: every fused multiply-add
+// here is written out, and no other pair of operations may be fused.
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "mgopt.h"
+
+namespace {
+
+constexpr int kBlock = 256;          // work-group size of the streaming passes
+constexpr int kFinalizeBlock = 1024; // single work-group of the finalize kernel
+constexpr int kVec = 4;              // elements per thread per access (16 B of fp32)
+constexpr int kStagingSlots = 4;     // pinned host buffers for grad-pointer uploads
+
+struct DevTensor {
+    float* param;   // fp32 param or fp32 master
+    void* lowp;     // bf16/fp16 model param or nullptr
+    float* m;
+    float* v;
+    int64_t numel;
+    int32_t group;
+    int32_t pad;
+};
+
+struct Chunk {
+    uint32_t tensor;
+    uint32_t index;  // chunk number inside its tensor; start = index * chunk_elems
+};
+
+struct Partial {
+    double sumsq;
+    uint32_t nonfinite;
+    uint32_t pad;
+};
+
+struct GroupConst {
+    double lr, wd, beta1, beta2, eps;
+    int32_t maximize;
+    int32_t pad;
+};
+
+// ---------------------------------------------------------------------------
+// element conversions
+// ---------------------------------------------------------------------------
+
+template <typename T>
+struct GradIO;
+
+template <>
+struct GradIO<float> {
+    static __device__ __forceinline__ float to_f32(float x) { return x; }
+    static __device__ __forceinline__ float from_f32(float x) { return x; }
+};
+
+struct Bf16 {
+    uint16_t bits;
+};
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;  // NaN -> canonical quiet NaN
+    return static_cast<uint16_t>((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+template <>
+struct GradIO<Bf16> {
+    static __device__ __forceinline__ float to_f32(Bf16 x) { return __uint_as_float(static_cast<uint32_t>(x.bits) << 16); }
+    static __device__ __forceinline__ Bf16 from_f32(float x) { return Bf16{f32_to_bf16_rne(x)}; }
+};
+
+template <>
+struct GradIO<_Float16> {
+    static __device__ __forceinline__ float to_f32(_Float16 x) { return static_cast<float>(x); }
+    static __device__ __forceinline__ _Float16 from_f32(float x) { return static_cast<_Float16>(x); }
+};
+
+// Four consecutive elements of a 2-byte type travel as one 8-byte access,
+// four fp32 as one 16-byte access.
+template <typename T>
+struct Vec4 {
+    T e[4];
+};
+
+template <typename T>
+__device__ __forceinline__ Vec4<T> load4(const T* p) {
+    Vec4<T> r;
+    if constexpr (sizeof(T) == 4) {
+        const float4 q = *reinterpret_cast<const float4*>(p);
+        r.e[0] = reinterpret_cast<const T&>(q.x);
+        r.e[1] = reinterpret_cast<const T&>(q.y);
+        r.e[2] = reinterpret_cast<const T&>(q.z);
+        r.e[3] = reinterpret_cast<const T&>(q.w);
+    } else {
+        const uint2 q = *reinterpret_cast<const uint2*>(p);
+        uint16_t h[4] = {static_cast<uint16_t>(q.x & 0xFFFFu), static_cast<uint16_t>(q.x >> 16),
+                         static_cast<uint16_t>(q.y & 0xFFFFu), static_cast<uint16_t>(q.y >> 16)};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) std::memcpy(&r.e[k], &h[k], 2);
+    }
+    return r;
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const Vec4<T>& r) {
+    if constexpr (sizeof(T) == 4) {
+        float4 q;
+        q.x = reinterpret_cast<const float&>(r.e[0]);
+        q.y = reinterpret_cast<const float&>(r.e[1]);
+        q.z = reinterpret_cast<const float&>(r.e[2]);
+        q.w = reinterpret_cast<const float&>(r.e[3]);
+        *reinterpret_cast<float4*>(p) = q;
+    } else {
+        uint16_t h[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) std::memcpy(&h[k], &r.e[k], 2);
+        uint2 q;
+        q.x = static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16);
+        q.y = static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16);
+        *reinterpret_cast<uint2*>(p) = q;
+    }
+}
+
+__device__ __forceinline__ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// ---------------------------------------------------------------------------
+// pass 1: unscale + non-finite flag + sum of squares
+// ---------------------------------------------------------------------------
+
+struct NormArgs {
+    const DevTensor* tensors;
+    const Chunk* chunks;
+    const void* const* grads;
+    Partial* partials;
+    const float* scale;  // nullable
+    int64_t chunk_elems;
+    uint32_t chunk_begin;
+};
+
+__device__ __forceinline__ double wave_sum(double x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
+__device__ __forceinline__ uint32_t wave_or(uint32_t x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x |= __shfl_xor(x, off);
+    return x;
+}
+
+// Reduces (sum, flag) over a work-group of kBlock threads in a fixed order and
+// returns the result in thread 0.
+template <int NT>
+__device__ __forceinline__ void block_reduce(double& s, uint32_t& f) {
+    __shared__ double ws[NT / 64];
+    __shared__ uint32_t wf[NT / 64];
+    s = wave_sum(s);
+    f = wave_or(f);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        ws[wave] = s;
+        wf[wave] = f;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        uint32_t g = 0;
+#pragma unroll
+        for (int w = 0; w < NT / 64; ++w) {
+            t += ws[w];
+            g |= wf[w];
+        }
+        s = t;
+        f = g;
+    }
+}
+
+__device__ __forceinline__ void norm_accum(float x, float inv, bool unscale, double& acc, uint32_t& bad) {
+    // grad_scaler.py:280-284: the finiteness test is on the scaled input value
+    bad |= static_cast<uint32_t>(!isfinite(x));
+    const float u = unscale ? x * inv : x;
+    const double d = static_cast<double>(u);
+    acc = fma(d, d, acc);  // u*u is exact in double
+}
+
+template <typename GT>
+__global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
+    const uint32_t cidx = a.chunk_begin + blockIdx.x;
+    const Chunk ck = a.chunks[cidx];
+    const GT* __restrict__ g = static_cast<const GT*>(a.grads[ck.tensor]);
+    double acc = 0.0;
+    uint32_t bad = 0;
+    if (g != nullptr) {
+        const int64_t numel = a.tensors[ck.tensor].numel;
+        const int64_t start = static_cast<int64_t>(ck.index) * a.chunk_elems;
+        const int64_t len = min(a.chunk_elems, numel - start);
+        g += start;
+        const bool unscale = a.scale != nullptr;
+        const float inv = unscale ? static_cast<float>(1.0 / static_cast<double>(*a.scale)) : 1.0f;
+        int64_t done = 0;
+        if (aligned(g, sizeof(GT) * kVec)) {
+            const int64_t nvec = len / kVec;
+            int64_t i = threadIdx.x;
+            for (; i + kBlock < nvec; i += 2 * kBlock) {
+                const Vec4<GT> x0 = load4(g + i * kVec);
+                const Vec4<GT> x1 = load4(g + (i + kBlock) * kVec);
+#pragma unroll
+                for (int k = 0; k < kVec; ++k) norm_accum(GradIO<GT>::to_f32(x0.e[k]), inv, unscale, acc, bad);
+#pragma unroll
+                for (int k = 0; k < kVec; ++k) norm_accum(GradIO<GT>::to_f32(x1.e[k]), inv, unscale, acc, bad);
+            }
+            if (i < nvec) {
+                const Vec4<GT> x0 = load4(g + i * kVec);
+#pragma unroll
+                for (int k = 0; k < kVec; ++k) norm_accum(GradIO<GT>::to_f32(x0.e[k]), inv, unscale, acc, bad);
+            }
+            done = nvec * kVec;
+        }
+        for (int64_t i = done + threadIdx.x; i < len; i += kBlock) norm_accum(GradIO<GT>::to_f32(g[i]), inv, unscale, acc, bad);
+    }
+    block_reduce<kBlock>(acc, bad);
+    if (threadIdx.x == 0) {
+        Partial p;
+        p.sumsq = acc;
+        p.nonfinite = bad;
+        p.pad = 0;
+        a.partials[cidx] = p;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// finalize: total norm, clip coefficient, found_inf
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(kFinalizeBlock)
+    finalize_kernel(const Partial* partials, int64_t n, double max_norm, float* norm_out, float* coef_out,
+                    float* found_inf_out) {
+    double s = 0.0;
+    uint32_t f = 0;
+    for (int64_t i = threadIdx.x; i < n; i += kFinalizeBlock) {
+        s += partials[i].sumsq;
+        f |= partials[i].nonfinite;
+    }
+    block_reduce<kFinalizeBlock>(s, f);
+    if (threadIdx.x != 0) return;
+    // Norm of the stacked per-tensor norms = sqrt of the total sum of squares
+    // (clip_grad.py:96-108).  A sum beyond the fp32 range overflows to inf as
+    // torch's fp32 accumulation does.
+    float norm;
+    if (isnan(s)) norm = __builtin_nanf("");
+    else if (isinf(static_cast<float>(s))) norm = __builtin_inff();
+    else norm = static_cast<float>(sqrt(s));
+    if (norm_out) *norm_out = norm;
+    if (coef_out) {
+        // clip_grad.py:165-169 -> reciprocal(norm + 1e-6) * max_norm, clamp(max=1);
+        // NaN propagates through the clamp
+        const float d = norm + 1e-6f;
+        const float r = 1.0f / d;
+        float c = r * static_cast<float>(max_norm);
+        if (!isnan(c) && c > 1.0f) c = 1.0f;
+        *coef_out = c;
+    }
+    if (found_inf_out) *found_inf_out = f ? 1.0f : 0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// prologue: step counters
+// ---------------------------------------------------------------------------
+
+// adam.py:414 (step_t += 1) runs only when the step is taken: GradScaler skips
+// optimizer.step() on found_inf (grad_scaler.py:348-358); the fused path
+// subtracts found_inf back (adam.py:877-899).  Tensors without grad keep their
+// count (adam.py:153).
+__global__ void __launch_bounds__(kBlock)
+    prologue_kernel(const void* const* grads, float* steps, int32_t n, const float* found_inf) {
+    const int32_t i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n) return;
+    if (found_inf != nullptr && *found_inf != 0.0f) return;
+    if (grads[i] != nullptr) steps[i] = steps[i] + 1.0f;
+}
+
+// ---------------------------------------------------------------------------
+// pass 2: fused unscale + clip + AdamW
+// ---------------------------------------------------------------------------
+
+struct AdamArgs {
+    const DevTensor* tensors;
+    const Chunk* chunks;
+    void* const* grads;
+    const float* steps;
+    const double* bc;
+    int64_t bc_cap;
+    const float* scale;      // nullable
+    const float* coef;       // nullable
+    const float* found_inf;  // nullable
+    int* err;
+    int64_t chunk_elems;
+    uint32_t chunk_begin;
+    int32_t writeback;
+    GroupConst groups[MGOPT_MAX_GROUPS];
+};
+
+struct ElemConst {
+    float inv, coef, decay, w1, w1m1, b2, w2, bc2s, eps, nss;
+    bool unscale, clip, do_decay, small, maximize;
+};
+
+// One element of the step, in torch's order:
+//   grad_scaler.py:280-284  g = g * inv_scale              (unscale_)
+//   clip_grad.py:174        g = g * clip_coef              (clip_grad_norm_)
+//   adam.py:397             g = -g                         (maximize)
+//   adam.py:416-419         p = p * float(1 - lr*wd)
+//   adam.py:457             m = lerp(m, g, float(1-beta1)) as ATen's vector lerp
+//   adam.py:476             v = fma(float(1-beta2)*g, g, v*float(beta2))
+//   adam.py:542             d = sqrt(v) / float(sqrt(bc2)) + float(eps)
+//   adam.py:547             p = p + (float(-lr/bc1) * m) / d
+__device__ __forceinline__ float adam_elem(float g, float& p, float& m, float& v, const ElemConst& c) {
+    if (c.unscale) g = g * c.inv;
+    if (c.clip) g = g * c.coef;
+    const float gc = g;
+    if (c.maximize) g = -g;
+    if (c.do_decay) p = p * c.decay;
+    const float diff = g - m;
+    m = c.small ? __builtin_fmaf(c.w1, diff, m) : __builtin_fmaf(c.w1m1, diff, g);
+    v = v * c.b2;
+    v = __builtin_fmaf(c.w2 * g, g, v);
+    float d = __builtin_sqrtf(v);
+    d = d / c.bc2s;
+    d = d + c.eps;
+    float u = c.nss * m;
+    u = u / d;
+    p = p + u;
+    return gc;
+}
+
+template <int LOWP>
+struct LowpStore;
+template <>
+struct LowpStore<MGOPT_NONE> {
+    static __device__ __forceinline__ void store4(void*, const float*) {}
+    static __device__ __forceinline__ void store1(void*, float) {}
+};
+template <>
+struct LowpStore<MGOPT_BF16> {
+    static __device__ __forceinline__ void store4(void* p, const float* x) {
+        uint2 q;
+        q.x = static_cast<uint32_t>(f32_to_bf16_rne(x[0])) | (static_cast<uint32_t>(f32_to_bf16_rne(x[1])) << 16);
+        q.y = static_cast<uint32_t>(f32_to_bf16_rne(x[2])) | (static_cast<uint32_t>(f32_to_bf16_rne(x[3])) << 16);
+        *reinterpret_cast<uint2*>(p) = q;
+    }
+    static __device__ __forceinline__ void store1(void* p, float x) { *static_cast<uint16_t*>(p) = f32_to_bf16_rne(x); }
+};
+template <>
+struct LowpStore<MGOPT_F16> {
+    static __device__ __forceinline__ void store4(void* p, const float* x) {
+        Vec4<_Float16> h;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) h.e[k] = static_cast<_Float16>(x[k]);
+        ::store4(static_cast<_Float16*>(p), h);
+    }
+    static __device__ __forceinline__ void store1(void* p, float x) { *static_cast<_Float16*>(p) = static_cast<_Float16>(x); }
+};
+
+template <typename GT, int LOWP>
+__global__ void __launch_bounds__(kBlock) adamw_kernel(const AdamArgs a) {
+    const uint32_t cidx = a.chunk_begin + blockIdx.x;
+    const Chunk ck = a.chunks[cidx];
+    GT* __restrict__ g = static_cast<GT*>(a.grads[ck.tensor]);
+    if (g == nullptr) return;
+    if (a.found_inf != nullptr && *a.found_inf != 0.0f) return;  // skipped step
+    const DevTensor T = a.tensors[ck.tensor];
+    const GroupConst G = a.groups[T.group];
+    const int64_t t = static_cast<int64_t>(a.steps[ck.tensor]);
+    if (t < 1 || t >= a.bc_cap) {
+        if (threadIdx.x == 0) *a.err = 1;  // host table does not cover this step: leave the tensor untouched
+        return;
+    }
+    const double* bc = a.bc + (static_cast<int64_t>(T.group) * a.bc_cap + t) * 2;
+
+    ElemConst c;
+    c.unscale = a.scale != nullptr;
+    c.inv = c.unscale ? static_cast<float>(1.0 / static_cast<double>(*a.scale)) : 1.0f;
+    c.clip = a.coef != nullptr;
+    c.coef = c.clip ? *a.coef : 1.0f;
+    c.maximize = G.maximize != 0;
+    c.do_decay = G.wd != 0.0;
+    c.decay = static_cast<float>(1.0 - G.lr * G.wd);
+    c.w1 = static_cast<float>(1.0 - G.beta1);
+    c.w1m1 = c.w1 - 1.0f;
+    c.small = fabsf(c.w1) < 0.5f;
+    c.b2 = static_cast<float>(G.beta2);
+    c.w2 = static_cast<float>(1.0 - G.beta2);
+    c.bc2s = static_cast<float>(bc[1]);
+    c.eps = static_cast<float>(G.eps);
+    c.nss = static_cast<float>(-(G.lr / bc[0]));
+
+    const int64_t start = static_cast<int64_t>(ck.index) * a.chunk_elems;
+    const int64_t len = min(a.chunk_elems, T.numel - start);
+    float* __restrict__ P = T.param + start;
+    float* __restrict__ M = T.m + start;
+    float* __restrict__ V = T.v + start;
+    g += start;
+    void* L = nullptr;
+    if constexpr (LOWP != MGOPT_NONE) L = static_cast<uint16_t*>(T.lowp) + start;
+    const bool wb = a.writeback != 0;
+
+    int64_t done = 0;
+    const bool vec = aligned(P, 16) && aligned(M, 16) && aligned(V, 16) && aligned(g, sizeof(GT) * kVec) &&
+                     (LOWP == MGOPT_NONE || aligned(L, 8));
+    if (vec) {
+        const int64_t nvec = len / kVec;
+        for (int64_t i = threadIdx.x; i < nvec; i += kBlock) {
+            const int64_t e = i * kVec;
+            const Vec4<GT> gv = load4(g + e);
+            float4 p = *reinterpret_cast<const float4*>(P + e);
+            float4 m = *reinterpret_cast<const float4*>(M + e);
+            float4 v = *reinterpret_cast<const float4*>(V + e);
+            Vec4<GT> go;
+            go.e[0] = GradIO<GT>::from_f32(adam_elem(GradIO<GT>::to_f32(gv.e[0]), p.x, m.x, v.x, c));
+            go.e[1] = GradIO<GT>::from_f32(adam_elem(GradIO<GT>::to_f32(gv.e[1]), p.y, m.y, v.y, c));
+            go.e[2] = GradIO<GT>::from_f32(adam_elem(GradIO<GT>::to_f32(gv.e[2]), p.z, m.z, v.z, c));
+            go.e[3] = GradIO<GT>::from_f32(adam_elem(GradIO<GT>::to_f32(gv.e[3]), p.w, m.w, v.w, c));
+            *reinterpret_cast<float4*>(P + e) = p;
+            *reinterpret_cast<float4*>(M + e) = m;
+            *reinterpret_cast<float4*>(V + e) = v;
+            if constexpr (LOWP != MGOPT_NONE) {
+                const float pf[4] = {p.x, p.y, p.z, p.w};
+                LowpStore<LOWP>::store4(static_cast<uint16_t*>(L) + e, pf);
+            }
+            if (wb) store4(g + e, go);
+        }
+        done = nvec * kVec;
+    }
+    for (int64_t i = done + threadIdx.x; i < len; i += kBlock) {
+        float p = P[i], m = M[i], v = V[i];
+        const float gc = adam_elem(GradIO<GT>::to_f32(g[i]), p, m, v, c);
+        P[i] = p;
+        M[i] = m;
+        V[i] = v;
+        if constexpr (LOWP != MGOPT_NONE) LowpStore<LOWP>::store1(static_cast<uint16_t*>(L) + i, p);
+        if (wb) g[i] = GradIO<GT>::from_f32(gc);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GradScaler.update
+// ---------------------------------------------------------------------------
+
+struct FoundList {
+    const float* p[8];
+};
+
+// grad_scaler.py:517-536: found_inf_combined = sum of the per-optimizer flags
+// (fp32, in order); torch._amp_update_scale_ then backs off on any nonzero
+// value (NaN included) or counts a good step, growing after growth_interval of
+// them unless the product overflows.  Factor products in double, rounded once.
+__global__ void scaler_kernel(float* scale, int32_t* tracker, FoundList fl, int32_t n, double growth, double backoff,
+                              int32_t interval) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    float fi = *fl.p[0];
+    for (int k = 1; k < n; ++k) fi = fi + *fl.p[k];
+    if (fi != 0.0f) {
+        *scale = static_cast<float>(static_cast<double>(*scale) * backoff);
+        *tracker = 0;
+    } else {
+        const int32_t ok = *tracker + 1;
+        if (ok == interval) {
+            const float ns = static_cast<float>(static_cast<double>(*scale) * growth);
+            if (isfinite(ns)) *scale = ns;
+            *tracker = 0;
+        } else {
+            *tracker = ok;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// grad scaling for the stand-alone clip path, master sync, synthetic data
+// ---------------------------------------------------------------------------
+
+template <typename GT>
+__global__ void __launch_bounds__(kBlock)
+    scale_grads_kernel(const DevTensor* tensors, const Chunk* chunks, void* const* grads, const float* coefp,
+                       int64_t chunk_elems, uint32_t chunk_begin) {
+    const Chunk ck = chunks[chunk_begin + blockIdx.x];
+    GT* g = static_cast<GT*>(grads[ck.tensor]);
+    if (g == nullptr) return;
+    const float coef = *coefp;
+    const int64_t start = static_cast<int64_t>(ck.index) * chunk_elems;
+    const int64_t len = min(chunk_elems, tensors[ck.tensor].numel - start);
+    g += start;
+    for (int64_t i = threadIdx.x; i < len; i += kBlock) g[i] = GradIO<GT>::from_f32(GradIO<GT>::to_f32(g[i]) * coef);
+}
+
+template <typename LT>
+__global__ void __launch_bounds__(kBlock)
+    sync_master_kernel(const DevTensor* tensors, const Chunk* chunks, int64_t chunk_elems, uint32_t chunk_begin) {
+    const Chunk ck = chunks[chunk_begin + blockIdx.x];
+    const DevTensor T = tensors[ck.tensor];
+    const int64_t start = static_cast<int64_t>(ck.index) * chunk_elems;
+    const int64_t len = min(chunk_elems, T.numel - start);
+    const LT* l = static_cast<const LT*>(T.lowp) + start;
+    float* p = T.param + start;
+    for (int64_t i = threadIdx.x; i < len; i += kBlock) p[i] = GradIO<LT>::to_f32(l[i]);
+}
+
+__device__ __host__ __forceinline__ uint64_t mix64(uint64_t x) {
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+constexpr uint64_t kGamma = 0x9E3779B97F4A7C15ull;
+
+template <typename T>
+__global__ void __launch_bounds__(kBlock)
+    synth_kernel(T* dst, int64_t n, uint64_t key, double k, uint64_t tail_every, double tail_mult) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        const uint64_t h = mix64(key + (static_cast<uint64_t>(i) + 1ull) * kGamma);
+        const int32_t s = static_cast<int32_t>(h & 0xFFFFu) + static_cast<int32_t>((h >> 16) & 0xFFFFu) +
+                          static_cast<int32_t>((h >> 32) & 0xFFFFu) + static_cast<int32_t>(h >> 48) - 131070;
+        double x = static_cast<double>(s) * k;
+        if (tail_every) {
+            const uint64_t h2 = mix64(h ^ 0xD1B54A32D192ED03ull);
+            if (h2 % tail_every == 0) x = x * tail_mult;
+        }
+        dst[i] = GradIO<T>::from_f32(static_cast<float>(x));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(static_cast<int>(e), std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr)                                   \
+    do {                                                \
+        hipError_t _e = (expr);                         \
+        if (_e != hipSuccess) return hip_fail(_e, #expr); \
+    } while (0)
+
+// Runs the body with the plan's device current, restoring the caller's.
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = false;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) == hipSuccess) ok = (prev == dev) || hipSetDevice(dev) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+}  // namespace
+
+struct mgopt_plan {
+    int device = 0;
+    int32_t n_tensors = 0;
+    int32_t n_groups = 0;
+    int64_t chunk_elems = 0;
+    int64_t n_chunks = 0;
+    DevTensor* d_tensors = nullptr;
+    Chunk* d_chunks = nullptr;
+    void** d_grads = nullptr;
+    Partial* d_partials = nullptr;
+    int* d_err = nullptr;
+    float* d_steps = nullptr;
+    struct Class {
+        int32_t grad_dtype;
+        int32_t lowp_dtype;
+        uint32_t begin;
+        uint32_t count;
+    };
+    std::vector<Class> classes;
+    bool has_state = false;  // false: grads-only plan (norm and grad scaling only)
+    std::vector<const void*> cached;
+    bool grads_uploaded = false;
+    void* staging[kStagingSlots] = {};
+    hipEvent_t staging_ev[kStagingSlots] = {};
+    bool staging_used[kStagingSlots] = {};
+    int slot = 0;
+};
+
+namespace {
+
+int launch_check(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, what);
+    return 0;
+}
+
+template <typename GT>
+int launch_norm(const mgopt_plan* P, const mgopt_plan::Class& c, const float* scale, hipStream_t s) {
+    NormArgs a{P->d_tensors, P->d_chunks, P->d_grads, P->d_partials, scale, P->chunk_elems, c.begin};
+    hipLaunchKernelGGL(norm_kernel<GT>, dim3(c.count), dim3(kBlock), 0, s, a);
+    return launch_check("norm_kernel");
+}
+
+template <typename GT, int LOWP>
+int launch_adamw(const AdamArgs& a, uint32_t count, hipStream_t s) {
+    hipLaunchKernelGGL((adamw_kernel<GT, LOWP>), dim3(count), dim3(kBlock), 0, s, a);
+    return launch_check("adamw_kernel");
+}
+
+template <typename GT>
+int launch_adamw_lowp(const AdamArgs& a, int32_t lowp, uint32_t count, hipStream_t s) {
+    switch (lowp) {
+        case MGOPT_NONE: return launch_adamw<GT, MGOPT_NONE>(a, count, s);
+        case MGOPT_BF16: return launch_adamw<GT, MGOPT_BF16>(a, count, s);
+        case MGOPT_F16: return launch_adamw<GT, MGOPT_F16>(a, count, s);
+        default: return fail(MGOPT_E_INVALID, "unknown lowp dtype");
+    }
+}
+
+int dtype_size(int32_t dt) {
+    switch (dt) {
+        case MGOPT_F32: return 4;
+        case MGOPT_F16:
+        case MGOPT_BF16: return 2;
+        default: return 0;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+MGOPT_API const char* mgopt_last_error(void) { return g_last_error.c_str(); }
+
+MGOPT_API const char* mgopt_version(void) { return "mgopt 0.1 gfx950"; }
+
+MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensors, int32_t n_groups, float* steps_dev,
+                                int64_t chunk_elems, mgopt_plan** out) {
+    if (!out) return fail(MGOPT_E_INVALID, "out is NULL");
+    *out = nullptr;
+    if (n_tensors <= 0 || !descs) return fail(MGOPT_E_INVALID, "empty tensor list");
+    if (n_groups <= 0 || n_groups > MGOPT_MAX_GROUPS) return fail(MGOPT_E_LIMIT, "n_groups must be in 1..16");
+    if (chunk_elems <= 0 || chunk_elems % 4096 != 0 || chunk_elems > (int64_t(1) << 30))
+        return fail(MGOPT_E_INVALID, "chunk_elems must be a positive multiple of 4096, at most 2^30");
+
+    // Validate and bucket tensors by (grad dtype, lowp dtype): one kernel instance per bucket.
+    std::vector<std::vector<int32_t>> buckets(9);
+    auto bucket_of = [](int32_t gd, int32_t ld) { return gd * 3 + (ld == MGOPT_NONE ? 0 : (ld == MGOPT_BF16 ? 1 : 2)); };
+    std::vector<DevTensor> host_t(n_tensors);
+    bool grads_only = false, with_state = false;
+    for (int32_t i = 0; i < n_tensors; ++i) {
+        const mgopt_tensor_desc& d = descs[i];
+        if (d.numel < 0) return fail(MGOPT_E_INVALID, "tensor " + std::to_string(i) + ": negative numel");
+        const bool none = !d.param_dev && !d.exp_avg_dev && !d.exp_avg_sq_dev && !d.lowp_dev;
+        const bool all = d.param_dev && d.exp_avg_dev && d.exp_avg_sq_dev;
+        if (d.numel > 0 && !none && !all)
+            return fail(MGOPT_E_INVALID, "tensor " + std::to_string(i) + ": set all of param/exp_avg/exp_avg_sq or none");
+        if (d.numel > 0 && none) grads_only = true;
+        if (d.numel > 0 && all) with_state = true;
+        if (d.group < 0 || d.group >= n_groups) return fail(MGOPT_E_INVALID, "tensor " + std::to_string(i) + ": bad group");
+        if (dtype_size(d.grad_dtype) == 0) return fail(MGOPT_E_INVALID, "tensor " + std::to_string(i) + ": bad grad dtype");
+        if (d.lowp_dtype != MGOPT_NONE && d.lowp_dtype != MGOPT_BF16 && d.lowp_dtype != MGOPT_F16)
+            return fail(MGOPT_E_INVALID, "tensor " + std::to_string(i) + ": bad lowp dtype");
+        if ((d.lowp_dtype == MGOPT_NONE) != (d.lowp_dev == nullptr) && d.numel > 0 && all)
+            return fail(MGOPT_E_INVALID, "tensor " + std::to_string(i) + ": lowp_dev and lowp_dtype disagree");
+        if (d.numel >= (int64_t(1) << 31) * chunk_elems)
+            return fail(MGOPT_E_LIMIT, "tensor " + std::to_string(i) + ": too many chunks");
+        const int32_t lowp = all ? d.lowp_dtype : MGOPT_NONE;
+        host_t[i] = DevTensor{d.param_dev, all ? d.lowp_dev : nullptr, d.exp_avg_dev, d.exp_avg_sq_dev, d.numel, d.group, 0};
+        buckets[bucket_of(d.grad_dtype, lowp)].push_back(i);
+    }
+    if (grads_only && with_state) return fail(MGOPT_E_INVALID, "a plan is either grads-only or has optimizer state for every tensor");
+    if (with_state && !steps_dev) return fail(MGOPT_E_INVALID, "steps_dev is NULL");
+
+    std::vector<Chunk> chunks;
+    mgopt_plan* P = new mgopt_plan();
+    P->n_tensors = n_tensors;
+    P->n_groups = n_groups;
+    P->chunk_elems = chunk_elems;
+    P->d_steps = steps_dev;
+    P->has_state = with_state;
+    for (int b = 0; b < 9; ++b) {
+        if (buckets[b].empty()) continue;
+        mgopt_plan::Class c;
+        c.grad_dtype = b / 3;
+        const int l = b % 3;
+        c.lowp_dtype = l == 0 ? MGOPT_NONE : (l == 1 ? MGOPT_BF16 : MGOPT_F16);
+        c.begin = static_cast<uint32_t>(chunks.size());
+        for (int32_t i : buckets[b]) {
+            const int64_t nch = (descs[i].numel + chunk_elems - 1) / chunk_elems;
+            for (int64_t k = 0; k < nch; ++k) chunks.push_back(Chunk{static_cast<uint32_t>(i), static_cast<uint32_t>(k)});
+        }
+        c.count = static_cast<uint32_t>(chunks.size() - c.begin);
+        if (c.count) P->classes.push_back(c);
+        if (chunks.size() > 0xFFFFFFF0ull) {
+            delete P;
+            return fail(MGOPT_E_LIMIT, "too many chunks");
+        }
+    }
+    P->n_chunks = static_cast<int64_t>(chunks.size());
+
+    auto cleanup = [&](int rc) {
+        mgopt_plan_destroy(P);
+        return rc;
+    };
+    if (hipGetDevice(&P->device) != hipSuccess) return cleanup(fail(MGOPT_E_INVALID, "no current HIP device"));
+    hipError_t e;
+    if ((e = hipMalloc(&P->d_tensors, sizeof(DevTensor) * n_tensors)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc tensors"));
+    if ((e = hipMalloc(&P->d_grads, sizeof(void*) * n_tensors)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc grads"));
+    if ((e = hipMalloc(&P->d_err, sizeof(int))) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc err"));
+    if (P->n_chunks > 0) {
+        if ((e = hipMalloc(&P->d_chunks, sizeof(Chunk) * P->n_chunks)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc chunks"));
+        if ((e = hipMalloc(&P->d_partials, sizeof(Partial) * P->n_chunks)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc partials"));
+        if ((e = hipMemcpy(P->d_chunks, chunks.data(), sizeof(Chunk) * P->n_chunks, hipMemcpyHostToDevice)) != hipSuccess)
+            return cleanup(hip_fail(e, "upload chunks"));
+    }
+    if ((e = hipMemcpy(P->d_tensors, host_t.data(), sizeof(DevTensor) * n_tensors, hipMemcpyHostToDevice)) != hipSuccess)
+        return cleanup(hip_fail(e, "upload tensors"));
+    if ((e = hipMemset(P->d_grads, 0, sizeof(void*) * n_tensors)) != hipSuccess) return cleanup(hip_fail(e, "clear grads"));
+    if ((e = hipMemset(P->d_err, 0, sizeof(int))) != hipSuccess) return cleanup(hip_fail(e, "clear err"));
+    for (int k = 0; k < kStagingSlots; ++k) {
+        if ((e = hipHostMalloc(&P->staging[k], sizeof(void*) * n_tensors, hipHostMallocDefault)) != hipSuccess)
+            return cleanup(hip_fail(e, "hipHostMalloc staging"));
+        if ((e = hipEventCreateWithFlags(&P->staging_ev[k], hipEventDisableTiming)) != hipSuccess)
+            return cleanup(hip_fail(e, "hipEventCreate"));
+    }
+    P->cached.assign(n_tensors, nullptr);
+    if ((e = hipDeviceSynchronize()) != hipSuccess) return cleanup(hip_fail(e, "plan upload"));
+    *out = P;
+    return 0;
+}
+
+MGOPT_API int mgopt_plan_destroy(mgopt_plan* P) {
+    if (!P) return 0;
+    DeviceGuard guard(P->device);
+    for (int k = 0; k < kStagingSlots; ++k) {
+        if (P->staging_ev[k]) {
+            (void)hipEventSynchronize(P->staging_ev[k]);
+            (void)hipEventDestroy(P->staging_ev[k]);
+        }
+        if (P->staging[k]) (void)hipHostFree(P->staging[k]);
+    }
+    // Kernels of this plan may still be queued: drain before freeing their tables.
+    (void)hipDeviceSynchronize();
+    (void)hipFree(P->d_tensors);
+    (void)hipFree(P->d_chunks);
+    (void)hipFree(P->d_grads);
+    (void)hipFree(P->d_partials);
+    (void)hipFree(P->d_err);
+    delete P;
+    return 0;
+}
+
+MGOPT_API int64_t mgopt_plan_num_chunks(const mgopt_plan* P) { return P ? P->n_chunks : -1; }
+
+MGOPT_API int mgopt_plan_set_grads(mgopt_plan* P, const void* const* grads_host, void* stream) {
+    if (!P || !grads_host) return fail(MGOPT_E_INVALID, "NULL argument");
+    if (P->grads_uploaded && std::memcmp(P->cached.data(), grads_host, sizeof(void*) * P->n_tensors) == 0) return 0;
+    DeviceGuard guard(P->device);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int k = P->slot;
+    // The staging slot may still feed an earlier copy; its event says when it is free.
+    if (P->staging_used[k]) HIP_TRY(hipEventSynchronize(P->staging_ev[k]));
+    std::memcpy(P->staging[k], grads_host, sizeof(void*) * P->n_tensors);
+    HIP_TRY(hipMemcpyAsync(P->d_grads, P->staging[k], sizeof(void*) * P->n_tensors, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipEventRecord(P->staging_ev[k], s));
+    P->staging_used[k] = true;
+    P->slot = (k + 1) % kStagingSlots;
+    std::memcpy(P->cached.data(), grads_host, sizeof(void*) * P->n_tensors);
+    P->grads_uploaded = true;
+    return 0;
+}
+
+MGOPT_API int mgopt_grad_norm(mgopt_plan* P, const float* scale_dev, double max_norm, float* norm_dev, float* coef_dev,
+                              float* found_inf_dev, void* stream) {
+    if (!P) return fail(MGOPT_E_INVALID, "NULL plan");
+    if (!P->grads_uploaded) return fail(MGOPT_E_INVALID, "mgopt_plan_set_grads was not called");
+    DeviceGuard guard(P->device);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (const auto& c : P->classes) {
+        int rc = 0;
+        switch (c.grad_dtype) {
+            case MGOPT_F32: rc = launch_norm<float>(P, c, scale_dev, s); break;
+            case MGOPT_F16: rc = launch_norm<_Float16>(P, c, scale_dev, s); break;
+            case MGOPT_BF16: rc = launch_norm<Bf16>(P, c, scale_dev, s); break;
+            default: rc = fail(MGOPT_E_INVALID, "bad grad dtype");
+        }
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(kFinalizeBlock), 0, s, P->d_partials, P->n_chunks, max_norm, norm_dev,
+                       coef_dev, found_inf_dev);
+    return launch_check("finalize_kernel");
+}
+
+MGOPT_API int mgopt_adamw_step(mgopt_plan* P, const mgopt_group_hparams* groups, const double* bc_dev, int64_t bc_cap,
+                               const float* scale_dev, const float* coef_dev, const float* found_inf_dev, int32_t flags,
+                               void* stream) {
+    if (!P || !groups || !bc_dev) return fail(MGOPT_E_INVALID, "NULL argument");
+    if (!P->has_state) return fail(MGOPT_E_INVALID, "grads-only plan: no optimizer state to update");
+    if (!P->grads_uploaded) return fail(MGOPT_E_INVALID, "mgopt_plan_set_grads was not called");
+    if (bc_cap < 2) return fail(MGOPT_E_INVALID, "bias-correction table too small");
+    DeviceGuard guard(P->device);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+
+    hipLaunchKernelGGL(prologue_kernel, dim3((P->n_tensors + kBlock - 1) / kBlock), dim3(kBlock), 0, s,
+                       const_cast<const void* const*>(P->d_grads), P->d_steps, P->n_tensors, found_inf_dev);
+    if (int rc = launch_check("prologue_kernel")) return rc;
+
+    AdamArgs a;
+    a.tensors = P->d_tensors;
+    a.chunks = P->d_chunks;
+    a.grads = P->d_grads;
+    a.steps = P->d_steps;
+    a.bc = bc_dev;
+    a.bc_cap = bc_cap;
+    a.scale = scale_dev;
+    a.coef = coef_dev;
+    a.found_inf = found_inf_dev;
+    a.err = P->d_err;
+    a.chunk_elems = P->chunk_elems;
+    a.writeback = (flags & MGOPT_WRITEBACK_GRADS) ? 1 : 0;
+    for (int gi = 0; gi < MGOPT_MAX_GROUPS; ++gi) {
+        GroupConst gc{};
+        if (gi < P->n_groups) {
+            gc.lr = groups[gi].lr;
+            gc.wd = groups[gi].weight_decay;
+            gc.beta1 = groups[gi].beta1;
+            gc.beta2 = groups[gi].beta2;
+            gc.eps = groups[gi].eps;
+            gc.maximize = groups[gi].maximize;
+        }
+        a.groups[gi] = gc;
+    }
+    for (const auto& c : P->classes) {
+        a.chunk_begin = c.begin;
+        int rc = 0;
+        switch (c.grad_dtype) {
+            case MGOPT_F32: rc = launch_adamw_lowp<float>(a, c.lowp_dtype, c.count, s); break;
+            case MGOPT_F16: rc = launch_adamw_lowp<_Float16>(a, c.lowp_dtype, c.count, s); break;
+            case MGOPT_BF16: rc = launch_adamw_lowp<Bf16>(a, c.lowp_dtype, c.count, s); break;
+            default: rc = fail(MGOPT_E_INVALID, "bad grad dtype");
+        }
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+MGOPT_API int mgopt_scaler_update(float* scale_dev, int32_t* tracker_dev, const float* const* found_inf_devs, int32_t n_found,
+                                  double growth, double backoff, int32_t interval, void* stream) {
+    if (!scale_dev || !tracker_dev || !found_inf_devs) return fail(MGOPT_E_INVALID, "NULL argument");
+    if (n_found < 1 || n_found > 8) return fail(MGOPT_E_LIMIT, "n_found must be in 1..8");
+    FoundList fl{};
+    for (int k = 0; k < n_found; ++k) {
+        if (!found_inf_devs[k]) return fail(MGOPT_E_INVALID, "NULL found_inf");
+        fl.p[k] = found_inf_devs[k];
+    }
+    hipLaunchKernelGGL(scaler_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), scale_dev, tracker_dev, fl,
+                       n_found, growth, backoff, interval);
+    return launch_check("scaler_kernel");
+}
+
+MGOPT_API int mgopt_scale_grads(mgopt_plan* P, const float* coef_dev, void* stream) {
+    if (!P || !coef_dev) return fail(MGOPT_E_INVALID, "NULL argument");
+    if (!P->grads_uploaded) return fail(MGOPT_E_INVALID, "mgopt_plan_set_grads was not called");
+    DeviceGuard guard(P->device);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (const auto& c : P->classes) {
+        switch (c.grad_dtype) {
+            case MGOPT_F32:
+                hipLaunchKernelGGL(scale_grads_kernel<float>, dim3(c.count), dim3(kBlock), 0, s, P->d_tensors, P->d_chunks,
+                                   P->d_grads, coef_dev, P->chunk_elems, c.begin);
+                break;
+            case MGOPT_F16:
+                hipLaunchKernelGGL(scale_grads_kernel<_Float16>, dim3(c.count), dim3(kBlock), 0, s, P->d_tensors,
+                                   P->d_chunks, P->d_grads, coef_dev, P->chunk_elems, c.begin);
+                break;
+            case MGOPT_BF16:
+                hipLaunchKernelGGL(scale_grads_kernel<Bf16>, dim3(c.count), dim3(kBlock), 0, s, P->d_tensors, P->d_chunks,
+                                   P->d_grads, coef_dev, P->chunk_elems, c.begin);
+                break;
+            default: return fail(MGOPT_E_INVALID, "bad grad dtype");
+        }
+        if (int rc = launch_check("scale_grads_kernel")) return rc;
+    }
+    return 0;
+}
+
+MGOPT_API int mgopt_sync_master(mgopt_plan* P, void* stream) {
+    if (!P) return fail(MGOPT_E_INVALID, "NULL plan");
+    if (!P->has_state) return fail(MGOPT_E_INVALID, "grads-only plan: no master weights");
+    DeviceGuard guard(P->device);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (const auto& c : P->classes) {
+        if (c.lowp_dtype == MGOPT_BF16)
+            hipLaunchKernelGGL(sync_master_kernel<Bf16>, dim3(c.count), dim3(kBlock), 0, s, P->d_tensors, P->d_chunks,
+                               P->chunk_elems, c.begin);
+        else if (c.lowp_dtype == MGOPT_F16)
+            hipLaunchKernelGGL(sync_master_kernel<_Float16>, dim3(c.count), dim3(kBlock), 0, s, P->d_tensors, P->d_chunks,
+                               P->chunk_elems, c.begin);
+        else
+            continue;
+        if (int rc = launch_check("sync_master_kernel")) return rc;
+    }
+    return 0;
+}
+
+MGOPT_API int mgopt_plan_error_flag(mgopt_plan* P, int* out) {
+    if (!P || !out) return fail(MGOPT_E_INVALID, "NULL argument");
+    DeviceGuard guard(P->device);
+    HIP_TRY(hipMemcpy(out, P->d_err, sizeof(int), hipMemcpyDeviceToHost));
+    return 0;
+}
+
+MGOPT_API int mgopt_synth_fill(void* dst, int32_t dtype, int64_t n, uint64_t seed, uint64_t stream_id, double k,
+                               uint64_t tail_every, double tail_mult, void* stream) {
+    if (n < 0 || (n > 0 && !dst)) return fail(MGOPT_E_INVALID, "bad destination");
+    if (n == 0) return 0;
+    const uint64_t key = mix64(seed * kGamma + mix64(stream_id + kGamma));
+    const int64_t blocks64 = std::min<int64_t>((n + kBlock - 1) / kBlock, 256 * 64);
+    const dim3 grid(static_cast<unsigned>(blocks64));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (dtype) {
+        case MGOPT_F32:
+            hipLaunchKernelGGL(synth_kernel<float>, grid, dim3(kBlock), 0, s, static_cast<float*>(dst), n, key, k, tail_every, tail_mult);
+            break;
+        case MGOPT_F16:
+            hipLaunchKernelGGL(synth_kernel<_Float16>, grid, dim3(kBlock), 0, s, static_cast<_Float16*>(dst), n, key, k,
+                               tail_every, tail_mult);
+            break;
+        case MGOPT_BF16:
+            hipLaunchKernelGGL(synth_kernel<Bf16>, grid, dim3(kBlock), 0, s, static_cast<Bf16*>(dst), n, key, k, tail_every, tail_mult);
+            break;
+        default: return fail(MGOPT_E_INVALID, "bad dtype");
+    }
+    return launch_check("synth_kernel");
+}
+
+}  // extern "C"

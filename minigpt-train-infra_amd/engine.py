@@ -1,0 +1,360 @@
+"""Device state and launch sequencing for one AdamW instance.
+
+An engine owns, on one GPU:
+  - flat fp32 arenas for exp_avg and exp_avg_sq (and an fp32 master copy for
+    bf16/fp16 parameters), one 256-byte-aligned segment per parameter, whose
+    per-parameter views are what optimizer.state[p] holds;
+  - a float32 step counter per parameter (torch/optim/adam.py:168-176);
+  - device scalars found_inf and clip coefficient for the current iteration;
+  - per-group bias-correction tables (1 - beta1**t, (1 - beta2**t) ** 0.5),
+    computed on the host with the expressions of adam.py:529-536;
+  - a libmgopt plan (the device chunk table).
+
+Per iteration the engine records what the caller asked for (a pending
+unscale, a clip) and launches:
+  norm(max_norm)  -> mgopt_grad_norm  (pass 1 + finalize)
+  step()          -> mgopt_adamw_step (prologue + pass 2)
+No call waits for the GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Any, Sequence
+
+import torch
+
+from . import _native as N
+
+ALIGN_ELEMS = 64                    # 256 B of fp32 per arena segment
+DEFAULT_CHUNK = 65536               # elements per work-group in both passes
+BC_INITIAL_CAP = 1024               # first bias-correction table size (steps)
+
+
+def _align(n: int) -> int:
+    return (n + ALIGN_ELEMS - 1) // ALIGN_ELEMS * ALIGN_ELEMS
+
+
+def bias_correction_table(beta1: float, beta2: float, cap: int) -> list[float]:
+    """[bc1(t), sqrt(bc2)(t)] for t in 0..cap-1, formed exactly as
+    torch/optim/adam.py:529-536 forms them from step = state["step"].item()."""
+    out: list[float] = []
+    for t in range(cap):
+        step = float(t)
+        bias_correction1 = 1 - beta1**step
+        bias_correction2 = 1 - beta2**step
+        out.append(bias_correction1)
+        out.append(bias_correction2**0.5)
+    return out
+
+
+class _Engine:
+    def __init__(self, optimizer: torch.optim.Optimizer, master_weights: bool | None, chunk_elems: int | None):
+        self.opt = optimizer
+        self.params: list[torch.Tensor] = []
+        self.group_index: list[int] = []
+        seen: set[int] = set()
+        for gi, group in enumerate(optimizer.param_groups):
+            for p in group["params"]:
+                if id(p) in seen:
+                    raise ValueError("some parameters appear in more than one parameter group")
+                seen.add(id(p))
+                self.params.append(p)
+                self.group_index.append(gi)
+        if not self.params:
+            raise ValueError("optimizer got an empty parameter list")
+        if len(optimizer.param_groups) > N.MAX_GROUPS:
+            raise ValueError(f"at most {N.MAX_GROUPS} parameter groups are supported")
+        dev = self.params[0].device
+        if dev.type != "cuda":
+            raise RuntimeError("mgopt AdamW needs parameters on a ROCm GPU (device type 'cuda'); there is no CPU path")
+        for p in self.params:
+            if p.device != dev:
+                raise RuntimeError("all parameters must live on one GPU")
+            if not p.is_contiguous():
+                raise RuntimeError("mgopt AdamW needs contiguous parameters")
+            if p.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+                raise TypeError(f"unsupported parameter dtype {p.dtype}")
+        self.device = dev
+        self.chunk_elems = int(chunk_elems or DEFAULT_CHUNK)
+        lowp = [p.dtype != torch.float32 for p in self.params]
+        if master_weights is False and any(lowp):
+            raise ValueError("bf16/fp16 parameters need master_weights (fp32 master copy); master_weights=False is not supported")
+        self.has_master = any(lowp)
+
+        # arena layout
+        self.offsets: list[int] = []
+        total = 0
+        for p in self.params:
+            self.offsets.append(total)
+            total += _align(p.numel())
+        self.total = total
+        self.master_offsets: list[int | None] = []
+        mtotal = 0
+        for p, lp in zip(self.params, lowp):
+            if lp:
+                self.master_offsets.append(mtotal)
+                mtotal += _align(p.numel())
+            else:
+                self.master_offsets.append(None)
+        with torch.cuda.device(dev):
+            self.exp_avg = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
+            self.exp_avg_sq = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
+            self.master = torch.empty(max(mtotal, 1), dtype=torch.float32, device=dev) if self.has_master else None
+            self.steps = torch.zeros(len(self.params), dtype=torch.float32, device=dev)
+            self.found_inf = torch.zeros((), dtype=torch.float32, device=dev)
+            self.coef = torch.ones((), dtype=torch.float32, device=dev)
+        self.master_synced = not self.has_master
+
+        # views handed out through optimizer.state
+        self.views: list[dict[str, torch.Tensor]] = []
+        for i, p in enumerate(self.params):
+            off, n = self.offsets[i], p.numel()
+            v = {
+                "step": self.steps[i],
+                "exp_avg": self.exp_avg[off : off + n].view(p.shape),
+                "exp_avg_sq": self.exp_avg_sq[off : off + n].view(p.shape),
+            }
+            mo = self.master_offsets[i]
+            if mo is not None:
+                v["master_param"] = self.master[mo : mo + n].view(p.shape)
+            self.views.append(v)
+
+        self.param_ptrs = [p.data_ptr() for p in self.params]
+        self.plan: int | None = None
+        self.plan_grad_dtypes: tuple[int, ...] | None = None
+        self.grad_ptrs: list[int] | None = None
+        self.grad_source: list[torch.Tensor | None] | None = None
+        self.grad_source_checked = False
+        self.complete_keys: set[tuple[int, ...]] = set()   # id tuples of parameter lists equal to self.params
+        self.t_bound = 0                     # upper bound of any step count reachable next step
+        self.bc_cap = 0
+        self.bc_keys: list[tuple[float, float]] = []
+        self.bc_table: torch.Tensor | None = None
+        self.reset_iteration()
+
+    # ------------------------------------------------------------------ plan
+    def close(self) -> None:
+        if self.plan is not None:
+            N.load_library().mgopt_plan_destroy(ctypes.c_void_p(self.plan))
+            self.plan = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _build_plan(self, grad_dtypes: tuple[int, ...]) -> None:
+        self.close()
+        lib = N.lib()
+        descs = (N.TensorDesc * len(self.params))()
+        for i, p in enumerate(self.params):
+            d = descs[i]
+            off = self.offsets[i]
+            mo = self.master_offsets[i]
+            if mo is None:
+                d.param_dev = p.data_ptr()
+                d.lowp_dev = None
+                d.lowp_dtype = N.NONE
+            else:
+                d.param_dev = self.master.data_ptr() + 4 * mo
+                d.lowp_dev = p.data_ptr()
+                d.lowp_dtype = N.dtype_code(p.dtype)
+            d.exp_avg_dev = self.exp_avg.data_ptr() + 4 * off
+            d.exp_avg_sq_dev = self.exp_avg_sq.data_ptr() + 4 * off
+            d.numel = p.numel()
+            d.group = self.group_index[i]
+            d.grad_dtype = grad_dtypes[i]
+        plan = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            N.check(
+                lib.mgopt_plan_create(descs, len(self.params), len(self.opt.param_groups), self.steps.data_ptr(),
+                                      self.chunk_elems, ctypes.byref(plan)),
+                "mgopt_plan_create",
+            )
+        self.plan = plan.value
+        self.plan_grad_dtypes = grad_dtypes
+        self.grad_ptrs = None
+
+    def set_grad_source(self, grads: Sequence[torch.Tensor | None] | None) -> None:
+        if grads is not None:
+            grads = list(grads)
+            if len(grads) != len(self.params):
+                raise ValueError("need one gradient (or None) per parameter")
+            for g, p in zip(grads, self.params):
+                if g is not None and g.shape != p.shape:
+                    raise ValueError("gradient shape does not match its parameter")
+        self.grad_source = grads
+        self.grad_source_checked = False
+
+    def current_grads(self) -> list[torch.Tensor | None]:
+        if self.grad_source is not None:
+            return self.grad_source
+        return [p.grad for p in self.params]
+
+    def prepare(self) -> None:
+        """Validates pointers and uploads the grad table for this iteration."""
+        ptrs = [p.data_ptr() for p in self.params]
+        if ptrs != self.param_ptrs:
+            raise RuntimeError(
+                "a parameter's storage moved (param.data was replaced) after the optimizer was built; "
+                "copy new values in place with param.data.copy_() instead"
+            )
+        # a gradient source given with set_grad_source is a fixed set of
+        # tensors: validated and uploaded once
+        if self.grad_source is not None and self.grad_source_checked and self.plan is not None:
+            return
+        grads = self.current_grads()
+        gptrs = [0 if g is None else g.data_ptr() for g in grads]
+        if gptrs == self.grad_ptrs and self.plan is not None:
+            return
+        dtypes = []
+        for g, p in zip(grads, self.params):
+            if g is None:
+                dtypes.append(N.dtype_code(p.dtype))
+                continue
+            if g.is_sparse:
+                raise RuntimeError("mgopt AdamW does not support sparse gradients")
+            if g.device != self.device:
+                raise RuntimeError("gradient on a different device than its parameter")
+            if not g.is_contiguous():
+                raise RuntimeError("mgopt AdamW needs contiguous gradients")
+            if g.numel() != p.numel():
+                raise RuntimeError("gradient size does not match its parameter")
+            dtypes.append(N.dtype_code(g.dtype))
+        dtypes_t = tuple(dtypes)
+        if self.plan is None or dtypes_t != self.plan_grad_dtypes:
+            # tensors without a grad this step keep the dtype of the previous plan
+            if self.plan_grad_dtypes is not None:
+                dtypes_t = tuple(self.plan_grad_dtypes[i] if grads[i] is None else dtypes_t[i] for i in range(len(grads)))
+            if self.plan is None or dtypes_t != self.plan_grad_dtypes:
+                self._build_plan(dtypes_t)
+        arr = (ctypes.c_void_p * len(gptrs))(*[p or None for p in gptrs])
+        N.check(N.lib().mgopt_plan_set_grads(ctypes.c_void_p(self.plan), arr, ctypes.c_void_p(N.stream_handle(self.device))),
+                "mgopt_plan_set_grads")
+        self.grad_ptrs = gptrs
+        if self.grad_source is not None:
+            self.grad_source_checked = True
+
+    # ------------------------------------------------------- iteration state
+    def reset_iteration(self) -> None:
+        self.scale_src: torch.Tensor | None = None   # pending lazy unscale (GradScaler scale tensor)
+        self.norm_done = False
+        self.clip_pending = False
+
+    def request_unscale(self, scale: torch.Tensor) -> torch.Tensor:
+        """GradScaler.unscale_: deferred; returns the found_inf tensor the
+        coming pass 1 will fill."""
+        if scale.device != self.device or scale.dtype != torch.float32 or scale.numel() != 1:
+            raise RuntimeError("scale must be a float32 scalar on the optimizer's device")
+        self.scale_src = scale
+        self.norm_done = False
+        return self.found_inf
+
+    def _stream(self) -> ctypes.c_void_p:
+        return ctypes.c_void_p(N.stream_handle(self.device))
+
+    def norm(self, max_norm: float | None) -> torch.Tensor:
+        """Pass 1 + finalize; returns the pre-clip total norm (fresh 0-dim tensor)."""
+        if self.norm_done and self.clip_pending:
+            raise RuntimeError("clip_grad_norm_ was already called for this optimizer step")
+        self.prepare()
+        out = torch.empty((), dtype=torch.float32, device=self.device)
+        self._launch_norm(out, max_norm)
+        self.norm_done = True
+        self.clip_pending = max_norm is not None
+        return out
+
+    def _launch_norm(self, norm_out: torch.Tensor | None, max_norm: float | None) -> None:
+        """max_norm None: no clipping requested, the coefficient is not written."""
+        lib = N.lib()
+        scale = self.scale_src
+        N.check(
+            lib.mgopt_grad_norm(
+                ctypes.c_void_p(self.plan),
+                ctypes.c_void_p(scale.data_ptr() if scale is not None else None),
+                ctypes.c_double(float(max_norm) if max_norm is not None else 0.0),
+                ctypes.c_void_p(norm_out.data_ptr() if norm_out is not None else None),
+                ctypes.c_void_p(self.coef.data_ptr() if max_norm is not None else None),
+                ctypes.c_void_p(self.found_inf.data_ptr() if scale is not None else None),
+                self._stream(),
+            ),
+            "mgopt_grad_norm",
+        )
+
+    def _ensure_bc(self, groups: list[dict[str, Any]]) -> None:
+        keys = [(float(g["betas"][0]), float(g["betas"][1])) for g in groups]
+        need = self.t_bound + 2
+        if self.bc_table is not None and need <= self.bc_cap and keys == self.bc_keys:
+            return
+        cap = max(BC_INITIAL_CAP, self.bc_cap)
+        while cap < need:
+            cap *= 2
+        flat: list[float] = []
+        for b1, b2 in keys:
+            flat.extend(bias_correction_table(b1, b2, cap))
+        table = torch.tensor(flat, dtype=torch.float64).to(self.device)
+        self.bc_table, self.bc_cap, self.bc_keys = table, cap, keys
+
+    def sync_master(self) -> None:
+        """Copies bf16/fp16 parameters into the fp32 master (exact widening)."""
+        if not self.has_master:
+            return
+        if self.plan is None:
+            self.prepare()
+        N.check(N.lib().mgopt_sync_master(ctypes.c_void_p(self.plan), self._stream()), "mgopt_sync_master")
+        self.master_synced = True
+
+    def step(self, found_inf: torch.Tensor | None = None, grad_scale: torch.Tensor | None = None,
+             writeback: bool = False) -> None:
+        groups = self.opt.param_groups
+        self.prepare()
+        if not self.master_synced:
+            self.sync_master()
+        scale = self.scale_src
+        skip_src = None
+        if scale is not None:
+            if not self.norm_done:
+                self._launch_norm(None, None)   # found_inf only, no clipping
+            skip_src = self.found_inf
+        else:
+            if grad_scale is not None:
+                scale = grad_scale
+            skip_src = found_inf
+        hp = (N.GroupHparams * len(groups))()
+        for gi, g in enumerate(groups):
+            if g.get("amsgrad", False):
+                raise NotImplementedError("amsgrad is not supported by mgopt AdamW")
+            lr = g["lr"]
+            hp[gi].lr = float(lr.item() if isinstance(lr, torch.Tensor) else lr)
+            hp[gi].weight_decay = float(g["weight_decay"])
+            hp[gi].beta1 = float(g["betas"][0])
+            hp[gi].beta2 = float(g["betas"][1])
+            hp[gi].eps = float(g["eps"])
+            hp[gi].maximize = 1 if g.get("maximize", False) else 0
+        self.t_bound += 1
+        self._ensure_bc(groups)
+        flags = N.WRITEBACK_GRADS if writeback else 0
+        N.check(
+            N.lib().mgopt_adamw_step(
+                ctypes.c_void_p(self.plan), hp, ctypes.c_void_p(self.bc_table.data_ptr()), self.bc_cap,
+                ctypes.c_void_p(scale.data_ptr() if scale is not None else None),
+                ctypes.c_void_p(self.coef.data_ptr() if self.clip_pending else None),
+                ctypes.c_void_p(skip_src.data_ptr() if skip_src is not None else None),
+                flags, self._stream(),
+            ),
+            "mgopt_adamw_step",
+        )
+        self.reset_iteration()
+
+    def error_flag(self) -> int:
+        out = ctypes.c_int(0)
+        if self.plan is not None:
+            N.check(N.lib().mgopt_plan_error_flag(ctypes.c_void_p(self.plan), ctypes.byref(out)), "mgopt_plan_error_flag")
+        return out.value
+
+    def set_step_counts(self, counts: Sequence[float]) -> None:
+        self.steps.copy_(torch.tensor([float(c) for c in counts], dtype=torch.float32))
+        self.t_bound = int(math.ceil(max(counts))) if counts else 0

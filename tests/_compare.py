@@ -1,0 +1,54 @@
+"""Tolerances and comparison helpers shared by the tests.
+
+The bars (stated once, used everywhere):
+  - found_inf, skip decision, loss scale and growth tracker: bit-exact;
+  - params / master / exp_avg / exp_avg_sq (fp32): max relative error
+    max|a - b| / max|b| per tensor <= 1e-6 (RTOL_STATE);
+  - bf16 / fp16 model params: at most 1 unit in the last place (ULP_LOWP);
+  - gradient norm: relative error <= 1e-5 (RTOL_NORM).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+RTOL_STATE = 1e-6
+RTOL_NORM = 1e-5
+ULP_LOWP = 1
+
+
+def maxrel(a: np.ndarray, b: np.ndarray) -> float:
+    """max |a - b| / max |b| over one tensor (0 when both are all zero)."""
+    a64 = np.asarray(a, np.float64).ravel()
+    b64 = np.asarray(b, np.float64).ravel()
+    if a64.size == 0:
+        return 0.0
+    d = float(np.max(np.abs(a64 - b64)))
+    s = float(np.max(np.abs(b64)))
+    return d / s if s > 0 else d
+
+
+def exact_fraction(a: np.ndarray, b: np.ndarray) -> float:
+    a = np.asarray(a).ravel()
+    b = np.asarray(b).ravel()
+    if a.size == 0:
+        return 1.0
+    return float(np.mean(a.view(np.uint32) == b.view(np.uint32))) if a.dtype == np.float32 else float(np.mean(a == b))
+
+
+def ulp16(a_bits: np.ndarray, b_bits: np.ndarray) -> int:
+    """Largest distance in units in the last place between two arrays of
+    bf16/fp16 bit patterns (sign-magnitude mapped to a monotone integer line)."""
+    def line(h):
+        h = np.asarray(h, np.int64) & 0xFFFF
+        return np.where(h & 0x8000, -(h & 0x7FFF), h)
+
+    if np.size(a_bits) == 0:
+        return 0
+    return int(np.max(np.abs(line(a_bits) - line(b_bits))))
+
+
+def rel(a: float, b: float) -> float:
+    if a == b:
+        return 0.0
+    return abs(a - b) / max(abs(b), 1e-300)

@@ -1,0 +1,195 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle, on the
+workloads the optimizer step is specified on, and against torch's own CPU path
+where torch's arithmetic is exact enough to be a reference.
+
+Bars (tests/_compare.py): skip / found_inf / scale / tracker / step counts
+bit-exact; fp32 state max relative error <= 1e-6; bf16 params <= 1 ulp; grad
+norm <= 1e-5 relative.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests._compare import RTOL_NORM, RTOL_STATE, ULP_LOWP, exact_fraction, maxrel, rel, ulp16
+from tests._gpu_harness import Case, Pair, log, mg, syn
+
+pytestmark = pytest.mark.gpu
+
+SCALER_GPT2 = dict(init_scale=65536.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=2000)
+
+
+def check_pair(pair: Pair, indices=None, expect_exact=True, label=""):
+    """Compares norms, scale trajectory, step counts and final state."""
+    c = pair.case
+    norms = [float(t) for t in pair.norms_gpu]
+    exact_norms = 0
+    for s, (ng, out) in enumerate(zip(norms, pair.outs)):
+        no = out["norm"]
+        if math.isfinite(no):
+            assert rel(ng, no) <= RTOL_NORM, (label, s + 1, ng, no)
+            exact_norms += ng == no
+        else:
+            assert (math.isnan(no) and math.isnan(ng)) or ng == no, (label, s + 1, ng, no)
+            exact_norms += 1
+    if c.scaler:
+        gpu_scales = [float(t) for t in pair.scale_gpu]
+        assert gpu_scales == [o["scale"] for o in pair.outs], label
+        assert pair.scaler._get_growth_tracker() == pair.outs[-1]["tracker"]
+    idx = range(len(pair.params)) if indices is None else indices
+    worst = {"p": 0.0, "m": 0.0, "v": 0.0}
+    exact = []
+    for i in idx:
+        st = pair.gpu_state(i)
+        assert st["step"] == pair.orc.steps[i], (label, i)
+        for k, ref in (("p", pair.orc.p[i]), ("m", pair.orc.m[i]), ("v", pair.orc.v[i])):
+            r = maxrel(st[k], ref.ravel())
+            worst[k] = max(worst[k], r)
+            assert r <= RTOL_STATE, (label, k, i, r)
+            exact.append(exact_fraction(st[k], ref.ravel()))
+        if "lowp_bits" in st:
+            assert ulp16(st["lowp_bits"], pair.oracle_lowp_bits(i)) <= ULP_LOWP
+    log(f"[{label}] norms exact {exact_norms}/{len(norms)}; worst maxrel {worst}; "
+        f"bit-exact fraction min {min(exact) if exact else 1.0:.6f}")
+    if expect_exact:
+        assert min(exact) == 1.0, label
+    assert pair.opt._engine.error_flag() == 0
+
+
+def test_synthetic_fill_matches_oracle():
+    for dt in ("f32", "f16", "bf16"):
+        for n in (1, 3, 4097, 1_000_003):
+            t = torch.empty(n, dtype={"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[dt], device="cuda")
+            syn.fill_(t, 5, 77, 0.7, 100, 1000.0)
+            ref = O.synth(n, 5, 77, O.synth_k(0.7), 100, 1000.0)
+            if dt == "f32":
+                assert np.array_equal(t.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+            else:
+                bits = t.view(torch.int16).cpu().numpy().view(np.uint16)
+                assert np.array_equal(bits, O.to_f16(ref) if dt == "f16" else O.to_bf16(ref)), (dt, n)
+
+
+def test_tiny_cpu_workload_100_steps_bit_exact():
+    """MiniGPT tiny_cpu shapes (52 tensors, 822,016 fp32 params), grads
+    N(0,1e-3), AdamW lr 3e-4 cosine (warm-up 10), betas (0.9, 0.95), eps 1e-8,
+    wd 0.1 on matrices and embeddings, clip 1.0, 100 steps."""
+    log("case: minigpt_tiny_cpu 100 steps")
+    pair = Pair(Case(shapes=mg.paramsets.WORKLOADS["minigpt_tiny_cpu"](), steps=100, sigma=1e-3))
+    pair.run()
+    check_pair(pair, label="tiny_cpu")
+
+
+def test_tiny_cpu_workload_against_torch_cpu():
+    """Same workload, GPU against torch 2.10's own CPU AdamW + clip_grad_norm_
+    (the reference's path): fp32 state within 1e-6 after 100 steps."""
+    from oracle.torch_path import TorchReferencePath
+
+    log("case: minigpt_tiny_cpu vs torch cpu")
+    pair = Pair(Case(shapes=mg.paramsets.WORKLOADS["minigpt_tiny_cpu"](), steps=100, sigma=1e-3))
+    init = [p.detach().cpu().numpy() for p in pair.params]
+    hp = [dict(betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1), dict(betas=(0.9, 0.95), eps=1e-8, weight_decay=0.0)]
+    ref = TorchReferencePath(init, pair.group_of, hp, max_norm=1.0)
+    for s in range(1, 101):
+        lr = mg.cosine_lr(s - 1, *pair.case.lr_sched)
+        mg.set_optimizer_lr(pair.opt, lr)
+        pair.fill_grads(s)
+        ref.step([g.detach().cpu().numpy() for g in pair.current_grads()], lr)
+        pair.gpu_step()
+    torch.cuda.synchronize()
+    worst = 0.0
+    for i in range(len(pair.params)):
+        st = pair.gpu_state(i)
+        p, m, v, step = ref.state(i)
+        assert st["step"] == step
+        for a, b in ((st["p"], p), (st["m"], m), (st["v"], v)):
+            worst = max(worst, maxrel(a, b.ravel()))
+    log(f"[tiny_cpu vs torch cpu] worst maxrel {worst:.3e}")
+    assert worst <= RTOL_STATE
+
+
+def test_gpt2_small_fp16_grads_with_scaler():
+    """GPT-2-small shapes (148 tensors, 124,475,904 fp32 params), fp16 grads
+    N(0,1e-2) x scale, GradScaler 65536 / x2 per 2000 / x0.5, +inf injected at
+    one seeded element at steps 17 and 53, clip 1.0, 60 steps; the oracle
+    updates a subset of tensors (every 1-D tensor and three matrices)."""
+    shapes = mg.paramsets.WORKLOADS["gpt2_small"]()
+    rng = np.random.RandomState(17)
+    decay_n = sum(1 for _, s in shapes if len(s) >= 2)
+    inject = {}
+    for step in (17, 53):
+        ti = int(rng.randint(len(shapes)))
+        n = int(np.prod([s for _, s in shapes][0])) if ti == 0 else None
+        inject[step] = [(ti, 0, float("inf"))]
+    subset = [1, 4, 5] + list(range(decay_n, len(shapes)))
+    log("case: gpt2_small fp16 grads + scaler, 60 steps")
+    pair = Pair(Case(shapes=shapes, grad_dtype="f16", steps=60, sigma=1e-2, scaler=SCALER_GPT2,
+                     inject=inject, subset=subset, lr_sched=(6e-4, 6e-5, 10, 200)))
+    pair.run()
+    skipped = [s + 1 for s, o in enumerate(pair.outs) if o["skipped"]]
+    assert skipped == [17, 53]
+    assert [o["scale"] for o in pair.outs][16] == 32768.0 and pair.outs[-1]["scale"] == 16384.0
+    check_pair(pair, indices=subset, label="gpt2_small")
+
+
+def test_bf16_master_with_heavy_tail_clipping():
+    """bf16 params with fp32 master / m / v, bf16 grads N(0,1e-3) with 0.1% of
+    elements x100 so clipping at 1.0 is active every step; a narrower GPT
+    (4 layers, width 512, vocab 50304) for 100 steps; every tensor checked."""
+    shapes = mg.paramsets.minigpt_shapes(vocab=50304, block=1024, n_layer=4, n_embd=512)
+    log("case: bf16 master, heavy tail, 100 steps")
+    pair = Pair(Case(shapes=shapes, param_dtype="bf16", grad_dtype="bf16", steps=100, sigma=1e-3,
+                     tail=(1000, 100.0)))
+    pair.run()
+    assert all(o["norm"] > 1.0 for o in pair.outs)
+    check_pair(pair, label="bf16_master")
+    # the bf16 model copy is the round-to-nearest-even image of the master
+    for i in range(len(pair.params)):
+        st = pair.gpu_state(i)
+        assert np.array_equal(st["lowp_bits"], O.to_bf16(st["p"]))
+
+
+def test_ragged_tensor_list_scaler_dynamics():
+    """20,000 tensors with log-uniform sizes (rescaled to 20M elements here),
+    fp16 grads, GradScaler growth_interval 50, a NaN or inf in 1% of 2000
+    steps: the scale / tracker trajectory and every step counter must match
+    the state machine bit for bit."""
+    shapes = mg.paramsets.ragged_shapes(total=20_000_000)
+    rng = np.random.RandomState(11)
+    bad_steps = sorted(rng.choice(np.arange(1, 2001), 20, replace=False).tolist())
+    sc = dict(init_scale=65536.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=50)
+    log(f"case: ragged 20k tensors, 2000 steps, bad steps {bad_steps}")
+    pair = Pair(Case(shapes=shapes, grad_dtype="f16", steps=2000, sigma=1e-2, scaler=sc, max_norm=1.0,
+                     fresh_grads=False))
+    dev = torch.device("cuda:0")
+    grads = pair.current_grads()
+    for i, g in enumerate(grads):
+        syn.fill_(g, syn.GRAD_SEED, syn.grad_stream(1, i), 1e-2 * 65536)
+    expected_scale, tracker = 65536.0, 0
+    snapshots = []
+    for s in range(1, 2001):
+        restore = None
+        if s in bad_steps:
+            ti = int(rng.randint(len(grads)))
+            restore = (ti, grads[ti].view(-1)[0].clone())
+            grads[ti].view(-1)[0] = float("nan") if s % 2 else float("inf")
+        mg.set_optimizer_lr(pair.opt, 1e-4)
+        pair.gpu_step()
+        if restore is not None:
+            grads[restore[0]].view(-1)[0] = restore[1]
+        expected_scale, tracker = O.scaler_update(expected_scale, tracker, 1.0 if s in bad_steps else 0.0, 2.0, 0.5, 50)
+        if s % 100 == 0:
+            snapshots.append((s, expected_scale, tracker))
+    torch.cuda.synchronize()
+    gpu_scales = [float(t) for t in pair.scale_gpu]
+    for s, e, _ in snapshots:
+        assert gpu_scales[s - 1] == e, (s, gpu_scales[s - 1], e)
+    assert pair.scaler._get_growth_tracker() == tracker
+    steps = pair.opt._engine.steps.cpu().numpy()
+    assert np.all(steps == 2000 - len(bad_steps))
+    assert pair.opt._engine.error_flag() == 0
+    log(f"[ragged] final scale {gpu_scales[-1]} tracker {tracker}")
