@@ -18,6 +18,7 @@ Differences a caller can observe, all by design:
 
 from __future__ import annotations
 
+import weakref
 from collections import defaultdict
 from typing import Any, Iterable
 
@@ -26,8 +27,16 @@ from torch.utils.weak import WeakIdKeyDictionary
 
 from .engine import _Engine
 
-#: parameter -> engine of the AdamW instance that owns it (used by clip_grad_norm_)
-_ENGINE_OF: WeakIdKeyDictionary = WeakIdKeyDictionary()
+#: parameter -> weak reference to the AdamW that owns it, registered when the
+#: parameter is added to the optimizer (used by clip_grad_norm_)
+_OWNER: WeakIdKeyDictionary = WeakIdKeyDictionary()
+
+
+def engine_of(param: torch.Tensor) -> _Engine | None:
+    """The engine of the AdamW that owns `param` (created on first use), or None."""
+    ref = _OWNER.get(param)
+    opt = ref() if ref is not None else None
+    return None if opt is None else opt._get_engine()
 
 
 class _TrackedState(defaultdict):
@@ -138,8 +147,6 @@ class AdamW(torch.optim.Optimizer):
     def _get_engine(self) -> _Engine:
         if self._engine is None:
             self._engine = _Engine(self, self._master_weights, self._chunk_elems)
-            for p in self._engine.params:
-                _ENGINE_OF[p] = self._engine
         return self._engine
 
     def _reconcile_state(self) -> None:
@@ -217,10 +224,11 @@ class AdamW(torch.optim.Optimizer):
             writeback=self._writeback,
         )
         # torch creates state on a parameter's first step with a grad (adam.py:153-184)
-        for i, (p, g) in enumerate(zip(eng.params, grads)):
-            if g is not None and i not in self._installed:
-                dict.__setitem__(self.state, p, dict(eng.views[i]))
-                self._installed.add(i)
+        if len(self._installed) < len(eng.params):
+            for i, (p, g) in enumerate(zip(eng.params, grads)):
+                if g is not None and i not in self._installed:
+                    dict.__setitem__(self.state, p, dict(eng.views[i]))
+                    self._installed.add(i)
         return loss
 
     def zero_grad(self, set_to_none: bool = True) -> None:
@@ -243,6 +251,9 @@ class AdamW(torch.optim.Optimizer):
         if getattr(self, "_engine", None) is not None:
             raise RuntimeError("add_param_group after the first step is not supported; build the optimizer with all groups")
         super().add_param_group(param_group)
+        me = weakref.ref(self)
+        for p in self.param_groups[-1]["params"]:
+            _OWNER[p] = me
 
     def state_dict(self) -> dict[str, Any]:
         if self._state_dirty:

@@ -19,7 +19,7 @@ from typing import Iterable
 import torch
 
 from . import _native as N
-from .adamw import _ENGINE_OF
+from .adamw import engine_of
 
 _GRAD_PLANS: dict[tuple, tuple[int, list[int]]] = {}
 
@@ -92,18 +92,18 @@ def clip_grad_norm_(
     # Fast path: this exact parameter list was seen before and is the whole
     # parameter set of one optimizer (the train.py:486 call, every step).
     key = tuple(map(id, parameters))
-    eng = _ENGINE_OF.get(parameters[0]) if parameters else None
+    eng = engine_of(parameters[0]) if parameters else None
     if eng is not None and key in eng.complete_keys:
         total = eng.norm(max_norm)
         _check_finite(total, error_if_nonfinite)
         return total
 
-    engines = {id(e): e for p in parameters if (e := _ENGINE_OF.get(p)) is not None}
+    engines = {id(e): e for p in parameters if (e := engine_of(p)) is not None}
     if len(engines) == 1:
         eng = next(iter(engines.values()))
         grads = eng.current_grads()
         mine = {id(p) for p, g in zip(eng.params, grads) if g is not None}
-        given = {id(p) for p in parameters if _ENGINE_OF.get(p) is eng}
+        given = {id(p) for p in parameters if engine_of(p) is eng}
         given_with_grad = {i for i in given if i in mine}
         if len(given) == len(parameters) and given_with_grad == mine:
             if not mine:

@@ -141,6 +141,10 @@ class _Engine:
             self.plan = None
 
     def __del__(self):
+        import sys
+
+        if sys.is_finalizing():
+            return  # the HIP runtime may already be gone; the process releases everything
         try:
             self.close()
         except Exception:
@@ -195,7 +199,14 @@ class _Engine:
         return [p.grad for p in self.params]
 
     def prepare(self) -> None:
-        """Validates pointers and uploads the grad table for this iteration."""
+        """Validates pointers and uploads the grad table for this iteration
+        (once per iteration: the norm pass and the step share it)."""
+        if self.prepared:
+            return
+        self._prepare()
+        self.prepared = True
+
+    def _prepare(self) -> None:
         ptrs = [p.data_ptr() for p in self.params]
         if ptrs != self.param_ptrs:
             raise RuntimeError(
@@ -243,6 +254,7 @@ class _Engine:
         self.scale_src: torch.Tensor | None = None   # pending lazy unscale (GradScaler scale tensor)
         self.norm_done = False
         self.clip_pending = False
+        self.prepared = False
 
     def request_unscale(self, scale: torch.Tensor) -> torch.Tensor:
         """GradScaler.unscale_: deferred; returns the found_inf tensor the

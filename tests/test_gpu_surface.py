@@ -1,0 +1,307 @@
+"""GPU checks of the drop-in surface: the torch.optim / torch.amp behaviours a
+training loop relies on, each compared with the CPU oracle or with torch."""
+
+from __future__ import annotations
+
+import copy
+import io
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests._compare import RTOL_NORM, RTOL_STATE, exact_fraction, maxrel, rel
+from tests._gpu_harness import Case, Pair, host_grad, log, mg, syn, to_f32
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+HP = [dict(betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1), dict(betas=(0.9, 0.95), eps=1e-8, weight_decay=0.0)]
+
+
+def _params(shapes, dtype=torch.float32):
+    out = []
+    for i, s in enumerate(shapes):
+        p = torch.empty(s, dtype=dtype, device=DEV)
+        syn.fill_(p, syn.PARAM_SEED, syn.param_stream(i), 0.02)
+        out.append(torch.nn.Parameter(p))
+    return out
+
+
+def _grads(params, step, sigma, dtype=None):
+    for i, p in enumerate(params):
+        p.grad = torch.empty_like(p) if dtype is None else torch.empty(p.shape, dtype=dtype, device=DEV)
+        syn.fill_(p.grad, syn.GRAD_SEED, syn.grad_stream(step, i), sigma)
+
+
+def test_first_clip_takes_the_fused_path_and_leaves_grads():
+    params = _params([(300, 7), (33,)], torch.bfloat16)
+    opt = mg.AdamW([{"params": params[:1], "weight_decay": 0.1}, {"params": params[1:], "weight_decay": 0.0}], lr=1e-3)
+    _grads(params, 1, 0.5)  # norm > 1: clipping active
+    before = [p.grad.clone() for p in params]
+    norm = mg.clip_grad_norm_(params, 1.0)
+    opt.step()
+    torch.cuda.synchronize()
+    assert float(norm) > 1.0
+    for b, p in zip(before, params):
+        assert torch.equal(b, p.grad)  # read, never rewritten
+    assert opt._engine.complete_keys  # the fast path is armed for the next call
+
+
+def test_writeback_grads_stores_the_clipped_gradient():
+    params = _params([(1000,), (4097,)])
+    opt = mg.AdamW(params, lr=1e-3, writeback_grads=True)
+    sc = mg.GradScaler("cuda", init_scale=256.0)
+    sc.scale(torch.ones((), device=DEV))
+    _grads(params, 1, 0.3 * 256.0)
+    host = [p.grad.detach().cpu().numpy() for p in params]
+    sc.unscale_(opt)
+    norm = mg.clip_grad_norm_(params, 1.0)
+    sc.step(opt)
+    sc.update()
+    torch.cuda.synchronize()
+    inv = O.inv_scale(256.0)
+    un = [O.unscale(h, inv)[0] for h in host]
+    n = O.norm_from_sumsq(O.total_sumsq(un))
+    assert float(norm) == n
+    coef = O.clip_coef(n, 1.0)
+    for u, p in zip(un, params):
+        O.scale_(u, coef)
+        assert np.array_equal(p.grad.cpu().numpy().view(np.uint32), u.view(np.uint32))
+
+
+def test_standalone_clip_matches_torch_semantics():
+    """A parameter list no optimizer owns: norm, then grads scaled in place."""
+    params = _params([(64, 65), (3,), (100003,)])
+    _grads(params, 3, 0.1)
+    host = [p.grad.detach().cpu().numpy().copy() for p in params]
+    norm = mg.clip_grad_norm_(params, 0.5)
+    torch.cuda.synchronize()
+    n = O.norm_from_sumsq(O.total_sumsq(host))
+    assert float(norm) == n
+    coef = O.clip_coef(n, 0.5)
+    for h, p in zip(host, params):
+        O.scale_(h, coef)
+        assert np.array_equal(p.grad.cpu().numpy(), h)
+    # and torch's own (fp32-accumulated) norm agrees to its precision
+    pre = [p.grad.cpu() / coef for p in params]
+    t_norm = torch.nn.utils.get_total_norm(pre)
+    assert rel(float(norm), float(t_norm)) <= RTOL_NORM
+
+
+def test_grads_that_are_none_skip_their_tensor():
+    pair = Pair(Case(shapes=[("a", (40, 40)), ("b", (40,)), ("c", (17, 3))], steps=1))
+    p0, p1, p2 = pair.params
+    for s in range(1, 6):
+        mg.set_optimizer_lr(pair.opt, 1e-3)
+        pair.fill_grads(s)
+        if s in (2, 4):
+            p1.grad = None
+        grads = [host_grad(p.grad) if p.grad is not None else None for p in pair.params]
+        f32 = [None if g is None else to_f32(*g) for g in grads]
+        pair.outs.append(pair.orc.step(f32, 1e-3))
+        pair.norms_gpu.append(mg.clip_grad_norm_(pair.params, 1.0))
+        pair.opt.step()
+        pair.opt.zero_grad(set_to_none=True)
+    torch.cuda.synchronize()
+    assert [pair.gpu_state(i)["step"] for i in range(3)] == [5.0, 3.0, 5.0]
+    for i in range(3):
+        st = pair.gpu_state(i)
+        for k, ref in (("p", pair.orc.p[i]), ("m", pair.orc.m[i]), ("v", pair.orc.v[i])):
+            assert exact_fraction(st[k], ref.ravel()) == 1.0, (i, k)
+    for ng, out in zip(pair.norms_gpu, pair.outs):
+        assert float(ng) == out["norm"]
+
+
+def test_misaligned_views_and_odd_sizes():
+    """Parameters that start 4 bytes into their storage and sizes that are not
+    multiples of 4 run through the element-wise path of both passes."""
+    base = torch.empty(5 * 4096 + 3, device=DEV)
+    syn.fill_(base, syn.PARAM_SEED, 99, 0.02)
+    views = [torch.nn.Parameter(base[1:4097]), torch.nn.Parameter(base[4099:4099 + 9999])]
+    full = base.cpu().numpy()
+    init = [full[1:4097].copy(), full[4099:4099 + 9999].copy()]
+    opt = mg.AdamW(views, lr=1e-3, betas=(0.9, 0.95), weight_decay=0.1)
+    orc = O.OracleRun(init, [0, 0], [dict(betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)], max_norm=1.0)
+    gbase = torch.empty(5 * 4096 + 5, device=DEV)
+    for s in range(1, 8):
+        syn.fill_(gbase, syn.GRAD_SEED, 1000 + s, 0.05)
+        views[0].grad = gbase[3:4099]
+        views[1].grad = gbase[4101:4101 + 9999]
+        hg = gbase.cpu().numpy()
+        out = orc.step([hg[3:4099].copy(), hg[4101:4101 + 9999].copy()], 1e-3)
+        norm = mg.clip_grad_norm_(views, 1.0)
+        opt.step()
+        assert float(norm) == out["norm"]
+    torch.cuda.synchronize()
+    for i, v in enumerate(views):
+        st = opt.state[v]
+        assert exact_fraction(v.detach().cpu().numpy(), orc.p[i]) == 1.0
+        assert exact_fraction(st["exp_avg"].cpu().numpy(), orc.m[i]) == 1.0
+        assert exact_fraction(st["exp_avg_sq"].cpu().numpy(), orc.v[i]) == 1.0
+
+
+def test_hyperparameter_branches():
+    """beta1 <= 0.5 (the other lerp form), beta1 = 0.5 exactly, maximize,
+    large eps, per-group betas, against the oracle bit for bit."""
+    shapes = [(257, 5), (1000,), (3, 3, 3), (6,)]
+    params = _params(shapes)
+    groups = [
+        {"params": params[:2], "betas": (0.3, 0.5), "eps": 1e-3, "weight_decay": 0.5, "maximize": True},
+        {"params": params[2:], "betas": (0.5, 0.999), "eps": 1e-6, "weight_decay": 0.0},
+    ]
+    opt = mg.AdamW(groups, lr=1e-2)
+    init = [p.detach().cpu().numpy().copy() for p in params]
+    orc = O.OracleRun(init, [0, 0, 1, 1], [dict(betas=(0.3, 0.5), eps=1e-3, weight_decay=0.5, maximize=True),
+                                             dict(betas=(0.5, 0.999), eps=1e-6, weight_decay=0.0)], max_norm=None)
+    for s in range(1, 16):
+        lr = mg.cosine_lr(s - 1, 1e-2, 1e-3, 3, 15)
+        mg.set_optimizer_lr(opt, lr)
+        _grads(params, s, 1e-3)
+        orc.step([p.grad.cpu().numpy() for p in params], lr)
+        opt.step()
+    torch.cuda.synchronize()
+    for i, p in enumerate(params):
+        st = opt.state[p]
+        assert exact_fraction(p.detach().cpu().numpy(), orc.p[i]) == 1.0, i
+        assert exact_fraction(st["exp_avg"].cpu().numpy(), orc.m[i]) == 1.0, i
+        assert exact_fraction(st["exp_avg_sq"].cpu().numpy(), orc.v[i]) == 1.0, i
+
+
+def _train(opt, scaler, params, steps, start=1):
+    for s in range(start, start + steps):
+        mg.set_optimizer_lr(opt, mg.cosine_lr(s - 1, 3e-4, 3e-5, 3, 20))
+        _grads(params, s, 1e-2 * scaler.get_scale())
+        if s == 4:
+            params[0].grad.view(-1)[7] = float("inf")
+        scaler.unscale_(opt)
+        mg.clip_grad_norm_(params, 1.0)
+        scaler.step(opt)
+        scaler.update()
+
+
+def test_resume_is_bitwise_identical_to_continuous():
+    """The reference's resume check (tests/test_resume_consistency.py:76-147):
+    N steps straight vs a checkpoint at step k, a fresh optimizer and scaler
+    loaded from it, and the remaining steps; bf16 params with fp32 master."""
+    shapes = [(128, 64), (64,), (5000,)]
+
+    def make():
+        params = _params(shapes, torch.bfloat16)
+        opt = mg.AdamW([{"params": params[:1], "weight_decay": 0.1, "group_name": "decay"},
+                        {"params": params[1:], "weight_decay": 0.0, "group_name": "no_decay"}],
+                       lr=3e-4, betas=(0.9, 0.95))
+        sc = mg.GradScaler("cuda", init_scale=1024.0, growth_interval=3)
+        sc.scale(torch.ones((), device=DEV))
+        return params, opt, sc
+
+    pa, oa, sa = make()
+    _train(oa, sa, pa, 8)
+    pb, ob, sb = make()
+    _train(ob, sb, pb, 5)
+    buf = io.BytesIO()
+    torch.save({"model": [p.detach().clone() for p in pb], "opt": ob.state_dict(), "scaler": sb.state_dict()}, buf)
+    buf.seek(0)
+    ck = torch.load(buf, weights_only=True)
+    pc, oc, scc = make()
+    with torch.no_grad():
+        for p, w in zip(pc, ck["model"]):
+            p.copy_(w)
+    oc.load_state_dict(ck["opt"])
+    scc.load_state_dict(ck["scaler"])
+    assert mg.optimizer_completed_steps(oc) == 4  # 5 iterations, one skipped on inf
+    _train(oc, scc, pc, 3, start=6)
+    torch.cuda.synchronize()
+    assert sa.state_dict() == scc.state_dict()
+    for x, y in zip(pa, pc):
+        assert torch.equal(x, y)
+    for x, y in zip(pa, pc):
+        for k in ("step", "exp_avg", "exp_avg_sq", "master_param"):
+            assert torch.equal(oa.state[x][k], oc.state[y][k]), k
+    sd = oc.state_dict()
+    assert [g["group_name"] for g in sd["param_groups"]] == ["decay", "no_decay"]
+    assert sd["state"][0]["exp_avg"].dtype == torch.float32
+
+
+def test_torch_adamw_state_dict_loads_and_continues():
+    """A torch.optim.AdamW checkpoint (CPU, fused=False) resumes here and the
+    continuation matches torch's own CPU continuation to 1e-6."""
+    shapes = [(50, 20), (20,)]
+    init = [O.synth(int(np.prod(s)), 1, i, O.synth_k(0.02)).reshape(s) for i, s in enumerate(shapes)]
+    cpu = [torch.nn.Parameter(torch.from_numpy(x.copy())) for x in init]
+    topt = torch.optim.AdamW(cpu, lr=1e-3, betas=(0.9, 0.95), weight_decay=0.1, fused=False)
+    gens = lambda s: [O.synth(int(np.prod(sh)), 2, (s << 20) | i, O.synth_k(1e-2)).reshape(sh) for i, sh in enumerate(shapes)]
+    for s in range(1, 4):
+        for p, g in zip(cpu, gens(s)):
+            p.grad = torch.from_numpy(g)
+        topt.step()
+    sd = copy.deepcopy(topt.state_dict())
+    gpu = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in cpu]
+    opt = mg.AdamW(gpu, lr=1e-3, betas=(0.9, 0.95), weight_decay=0.1)
+    opt.load_state_dict(sd)
+    for s in range(4, 8):
+        for p, q, g in zip(cpu, gpu, gens(s)):
+            p.grad = torch.from_numpy(g)
+            q.grad = torch.from_numpy(g).to(DEV)
+        topt.step()
+        opt.step()
+    torch.cuda.synchronize()
+    for p, q in zip(cpu, gpu):
+        assert maxrel(q.detach().cpu().numpy(), p.detach().numpy()) <= RTOL_STATE
+        for k in ("exp_avg", "exp_avg_sq"):
+            assert maxrel(opt.state[q][k].cpu().numpy(), topt.state[p][k].numpy()) <= RTOL_STATE
+        assert float(opt.state[q]["step"]) == float(topt.state[p]["step"]) == 7.0
+    # and the other way: this optimizer's state dict loads into torch's AdamW
+    back = torch.optim.AdamW([torch.nn.Parameter(q.detach().cpu()) for q in gpu], lr=1e-3)
+    back.load_state_dict({"state": {k: {n: t.cpu() for n, t in v.items()} for k, v in opt.state_dict()["state"].items()},
+                          "param_groups": opt.state_dict()["param_groups"]})
+
+
+def test_stock_torch_grad_scaler_drives_this_adamw():
+    """torch.amp.GradScaler hands found_inf / grad_scale to an optimizer with
+    _step_supports_amp_scaling; the results equal this package's scaler."""
+    shapes = [(300, 3), (77,)]
+    out = []
+    for use_stock in (False, True):
+        params = _params(shapes)
+        opt = mg.AdamW(params, lr=1e-3)
+        sc = torch.amp.GradScaler("cuda", init_scale=512.0, growth_interval=2) if use_stock else \
+            mg.GradScaler("cuda", init_scale=512.0, growth_interval=2)
+        sc.scale(torch.ones((), device=DEV))
+        for s in range(1, 7):
+            _grads(params, s, 1e-2 * sc.get_scale())
+            if s == 3:
+                params[1].grad[5] = float("nan")
+            sc.step(opt)   # no explicit unscale_: the scaler unscales inside step
+            sc.update()
+        torch.cuda.synchronize()
+        out.append(([p.detach().clone() for p in params], sc.get_scale()))
+    (pa, sa), (pb, sb) = out
+    assert sa == sb
+    for x, y in zip(pa, pb):
+        assert torch.equal(x, y)
+
+
+def test_scaler_stage_errors_match_torch():
+    params = _params([(10,)])
+    opt = mg.AdamW(params, lr=1e-3)
+    sc = mg.GradScaler("cuda")
+    with pytest.raises(AssertionError):
+        sc.unscale_(opt)  # scale() never called
+    sc.scale(torch.ones((), device=DEV))
+    _grads(params, 1, 1.0)
+    sc.unscale_(opt)
+    with pytest.raises(RuntimeError, match="already been called"):
+        sc.unscale_(opt)
+    sc.step(opt)
+    with pytest.raises(RuntimeError, match="after step"):
+        sc.unscale_(opt)
+    with pytest.raises(RuntimeError, match="already been called since the last update"):
+        sc.step(opt)
+    with pytest.raises(RuntimeError, match="Closure"):
+        sc.step(opt, closure=lambda: None)
+    sc.update()
+    with pytest.raises(AssertionError, match="No inf checks"):
+        sc.update()
+    st = sc.state_dict()
+    assert set(st) == {"scale", "growth_factor", "backoff_factor", "growth_interval", "_growth_tracker"}
