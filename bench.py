@@ -76,15 +76,18 @@ def time_cpu_baseline(name: str, budget_params: int) -> dict:
     from oracle.torch_path import time_reference_step
 
     shapes = mg.paramsets.WORKLOADS[name]()
+    # take tensors in model order (embeddings, then whole layers with their
+    # norm weights) until the budget is reached, skipping any single tensor
+    # that alone would overshoot it by more than half
     sample, n = [], 0
     for _, s in shapes:
         k = math.prod(s)
-        if n + k > budget_params and sample:
+        if n >= budget_params:
+            break
+        if n + k > 1.5 * budget_params and sample:
             continue
         sample.append(s)
         n += k
-        if n >= budget_params:
-            break
     total = sum(math.prod(s) for _, s in shapes)
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     r = time_reference_step(sample, steps=5, scaler=True, threads=threads)
@@ -121,7 +124,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="qwen3_8b", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-params", type=int, default=600_000_000)
+    ap.add_argument("--cpu-sample-params", type=int, default=1_000_000_000)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB fp32 device copy (reads 1 GiB, writes 1 GiB) three times, "
+                         "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (use --gpus 1)", file=sys.stderr)
@@ -129,6 +135,14 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30, "launches": 3}))
+        return 0
     spec, ordered, params, groups = build_workload(args.workload, dev)
     n_params = sum(p.numel() for p in params)
     log(f"workload {args.workload}: {len(params)} tensors, {n_params:,} params ({spec['param']} params, {spec['grad']} grads)")
@@ -144,10 +158,9 @@ def main() -> int:
         grads = [syn.fill_(torch.empty(p.shape, dtype=DT[spec["grad"]], device=dev), syn.GRAD_SEED,
                            syn.grad_stream(1, i), 1e-3 * init_scale) for i, p in enumerate(params)]
         opt.set_grad_source(grads)
-    torch.cuda.synchronize()
-    log(f"resident: {torch.cuda.memory_allocated(dev) / 1e9:.1f} GB after optimizer state allocation")
-
     eng = opt._get_engine()
+    torch.cuda.synchronize()
+    log(f"resident: {torch.cuda.memory_allocated(dev) / 1e9:.1f} GB (parameters, gradients, optimizer state)")
     stream = torch.cuda.current_stream(dev)
     ev = {"norm": [], "adamw": []}
 

@@ -31,10 +31,16 @@
 
 namespace {
 
-constexpr int kBlock = 256;          // work-group size of the streaming passes
+constexpr int kBlock = 512;          // work-group size of the streaming passes
 constexpr int kFinalizeBlock = 1024; // single work-group of the finalize kernel
 constexpr int kVec = 4;              // elements per thread per access (16 B of fp32)
 constexpr int kStagingSlots = 4;     // pinned host buffers for grad-pointer uploads
+// pass-2 access tuning (measured on MI355X with the Qwen3-8B-shaped set)
+constexpr int kUnroll = 1;           // 4-element accesses in flight per thread before use
+constexpr bool kNtLoad = true;       // nontemporal loads of grad/param/exp_avg/exp_avg_sq
+constexpr bool kNtStore = true;      // nontemporal stores of param/exp_avg/exp_avg_sq
+constexpr int kNormUnroll = 2;       // pass-1 4-element accesses in flight per thread
+constexpr bool kNtNormLoad = true;   // nontemporal gradient loads in pass 1
 
 struct DevTensor {
     float* param;   // fp32 param or fp32 master
@@ -146,6 +152,52 @@ __device__ __forceinline__ void store4(T* p, const Vec4<T>& r) {
 
 __device__ __forceinline__ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+// Native vector types for 16-byte (4 x fp32) and 8-byte (4 x 16-bit) accesses;
+// the nontemporal forms mark streamed data that no later access reuses.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <bool NT>
+__device__ __forceinline__ f32x4 ld16(const float* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    else return *reinterpret_cast<const f32x4*>(p);
+}
+template <bool NT>
+__device__ __forceinline__ void st16(float* p, f32x4 v) {
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+    else *reinterpret_cast<f32x4*>(p) = v;
+}
+template <bool NT>
+__device__ __forceinline__ u32x2 ld8(const void* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    else return *reinterpret_cast<const u32x2*>(p);
+}
+template <bool NT>
+__device__ __forceinline__ void st8(void* p, u32x2 v) {
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<u32x2*>(p));
+    else *reinterpret_cast<u32x2*>(p) = v;
+}
+
+// Four consecutive gradient elements widened to fp32.
+template <typename GT, bool NT>
+__device__ __forceinline__ void load_grad4(const GT* G, float out[4]) {
+    if constexpr (sizeof(GT) == 4) {
+        const f32x4 x = ld16<NT>(reinterpret_cast<const float*>(G));
+        out[0] = x.x; out[1] = x.y; out[2] = x.z; out[3] = x.w;
+    } else {
+        const u32x2 x = ld8<NT>(G);
+        const uint16_t h[4] = {static_cast<uint16_t>(x.x & 0xFFFFu), static_cast<uint16_t>(x.x >> 16),
+                               static_cast<uint16_t>(x.y & 0xFFFFu), static_cast<uint16_t>(x.y >> 16)};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            GT t;
+            std::memcpy(&t, &h[k], 2);
+            out[k] = GradIO<GT>::to_f32(t);
+        }
+    }
+}
+
+
 // ---------------------------------------------------------------------------
 // pass 1: unscale + non-finite flag + sum of squares
 // ---------------------------------------------------------------------------
@@ -225,18 +277,20 @@ __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
         if (aligned(g, sizeof(GT) * kVec)) {
             const int64_t nvec = len / kVec;
             int64_t i = threadIdx.x;
-            for (; i + kBlock < nvec; i += 2 * kBlock) {
-                const Vec4<GT> x0 = load4(g + i * kVec);
-                const Vec4<GT> x1 = load4(g + (i + kBlock) * kVec);
+            for (; i + (kNormUnroll - 1) * kBlock < nvec; i += kNormUnroll * kBlock) {
+                float x[kNormUnroll][4];
 #pragma unroll
-                for (int k = 0; k < kVec; ++k) norm_accum(GradIO<GT>::to_f32(x0.e[k]), inv, unscale, acc, bad);
+                for (int u = 0; u < kNormUnroll; ++u) load_grad4<GT, kNtNormLoad>(g + (i + u * kBlock) * kVec, x[u]);
 #pragma unroll
-                for (int k = 0; k < kVec; ++k) norm_accum(GradIO<GT>::to_f32(x1.e[k]), inv, unscale, acc, bad);
+                for (int u = 0; u < kNormUnroll; ++u)
+#pragma unroll
+                    for (int k = 0; k < kVec; ++k) norm_accum(x[u][k], inv, unscale, acc, bad);
             }
-            if (i < nvec) {
-                const Vec4<GT> x0 = load4(g + i * kVec);
+            for (; i < nvec; i += kBlock) {
+                float x[4];
+                load_grad4<GT, kNtNormLoad>(g + i * kVec, x);
 #pragma unroll
-                for (int k = 0; k < kVec; ++k) norm_accum(GradIO<GT>::to_f32(x0.e[k]), inv, unscale, acc, bad);
+                for (int k = 0; k < kVec; ++k) norm_accum(x[k], inv, unscale, acc, bad);
             }
             done = nvec * kVec;
         }
@@ -385,6 +439,35 @@ struct LowpStore<MGOPT_F16> {
     static __device__ __forceinline__ void store1(void* p, float x) { *static_cast<_Float16*>(p) = static_cast<_Float16>(x); }
 };
 
+// Four consecutive elements of one tensor through pass 2: load() issues the
+// memory reads, finish() does the arithmetic and the writes.
+template <typename GT>
+struct Quad {
+    float g[4];
+    f32x4 p, m, v;
+
+    __device__ __forceinline__ void load(const GT* G, const float* P, const float* M, const float* V, int64_t e) {
+        load_grad4<GT, kNtLoad>(G + e, g);
+        p = ld16<kNtLoad>(P + e);
+        m = ld16<kNtLoad>(M + e);
+        v = ld16<kNtLoad>(V + e);
+    }
+
+    template <int LOWP>
+    __device__ __forceinline__ void finish(GT* G, float* P, float* M, float* V, void* L, int64_t e, const ElemConst& c,
+                                           bool wb) {
+        float pf[4] = {p.x, p.y, p.z, p.w}, mf[4] = {m.x, m.y, m.z, m.w}, vf[4] = {v.x, v.y, v.z, v.w};
+        Vec4<GT> go;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) go.e[k] = GradIO<GT>::from_f32(adam_elem(g[k], pf[k], mf[k], vf[k], c));
+        st16<kNtStore>(P + e, f32x4{pf[0], pf[1], pf[2], pf[3]});
+        st16<kNtStore>(M + e, f32x4{mf[0], mf[1], mf[2], mf[3]});
+        st16<kNtStore>(V + e, f32x4{vf[0], vf[1], vf[2], vf[3]});
+        if constexpr (LOWP != MGOPT_NONE) LowpStore<LOWP>::store4(static_cast<uint16_t*>(L) + e, pf);
+        if (wb) store4(G + e, go);
+    }
+};
+
 template <typename GT, int LOWP>
 __global__ void __launch_bounds__(kBlock) adamw_kernel(const AdamArgs a) {
     const uint32_t cidx = a.chunk_begin + blockIdx.x;
@@ -432,26 +515,21 @@ __global__ void __launch_bounds__(kBlock) adamw_kernel(const AdamArgs a) {
     const bool vec = aligned(P, 16) && aligned(M, 16) && aligned(V, 16) && aligned(g, sizeof(GT) * kVec) &&
                      (LOWP == MGOPT_NONE || aligned(L, 8));
     if (vec) {
+        // four elements per thread per access; kUnroll accesses issued before
+        // the first one is consumed, to keep more bytes in flight per wave
         const int64_t nvec = len / kVec;
-        for (int64_t i = threadIdx.x; i < nvec; i += kBlock) {
-            const int64_t e = i * kVec;
-            const Vec4<GT> gv = load4(g + e);
-            float4 p = *reinterpret_cast<const float4*>(P + e);
-            float4 m = *reinterpret_cast<const float4*>(M + e);
-            float4 v = *reinterpret_cast<const float4*>(V + e);
-            Vec4<GT> go;
-            go.e[0] = GradIO<GT>::from_f32(adam_elem(GradIO<GT>::to_f32(gv.e[0]), p.x, m.x, v.x, c));
-            go.e[1] = GradIO<GT>::from_f32(adam_elem(GradIO<GT>::to_f32(gv.e[1]), p.y, m.y, v.y, c));
-            go.e[2] = GradIO<GT>::from_f32(adam_elem(GradIO<GT>::to_f32(gv.e[2]), p.z, m.z, v.z, c));
-            go.e[3] = GradIO<GT>::from_f32(adam_elem(GradIO<GT>::to_f32(gv.e[3]), p.w, m.w, v.w, c));
-            *reinterpret_cast<float4*>(P + e) = p;
-            *reinterpret_cast<float4*>(M + e) = m;
-            *reinterpret_cast<float4*>(V + e) = v;
-            if constexpr (LOWP != MGOPT_NONE) {
-                const float pf[4] = {p.x, p.y, p.z, p.w};
-                LowpStore<LOWP>::store4(static_cast<uint16_t*>(L) + e, pf);
-            }
-            if (wb) store4(g + e, go);
+        int64_t i = threadIdx.x;
+        for (; i + (kUnroll - 1) * kBlock < nvec; i += kUnroll * kBlock) {
+            Quad<GT> q[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) q[u].load(g, P, M, V, (i + u * kBlock) * kVec);
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) q[u].template finish<LOWP>(g, P, M, V, L, (i + u * kBlock) * kVec, c, wb);
+        }
+        for (; i < nvec; i += kBlock) {
+            Quad<GT> q;
+            q.load(g, P, M, V, i * kVec);
+            q.template finish<LOWP>(g, P, M, V, L, i * kVec, c, wb);
         }
         done = nvec * kVec;
     }
