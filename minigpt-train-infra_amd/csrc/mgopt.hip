@@ -33,7 +33,8 @@ namespace {
 
 constexpr int kBlock = 512;          // work-group size of the streaming passes
 constexpr int kFinalizeBlock = 1024; // single work-group of the finalize kernel
-constexpr int kVec = 4;              // elements per thread per access (16 B of fp32)
+constexpr int kVec = 4;              // elements per thread per access: 4 = one 16-B fp32 access per lane;
+                                     // 8 (two adjacent 16-B accesses) measured 1.8x slower (32-B lane stride)
 constexpr int kStagingSlots = 4;     // pinned host buffers for grad-pointer uploads
 // pass-2 access tuning (measured on MI355X with the Qwen3-8B-shaped set)
 constexpr int kUnroll = 1;           // 4-element accesses in flight per thread before use
@@ -178,22 +179,40 @@ __device__ __forceinline__ void st8(void* p, u32x2 v) {
     else *reinterpret_cast<u32x2*>(p) = v;
 }
 
-// Four consecutive gradient elements widened to fp32.
-template <typename GT, bool NT>
-__device__ __forceinline__ void load_grad4(const GT* G, float out[4]) {
+// W consecutive gradient elements widened to fp32 (W = 4 or 8): 16-byte
+// accesses for fp32 and for eight 16-bit values, an 8-byte access for four.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename GT>
+__device__ __forceinline__ void unpack16(uint32_t w, float* out) {
+    const uint16_t lo = static_cast<uint16_t>(w & 0xFFFFu), hi = static_cast<uint16_t>(w >> 16);
+    GT a, b;
+    std::memcpy(&a, &lo, 2);
+    std::memcpy(&b, &hi, 2);
+    out[0] = GradIO<GT>::to_f32(a);
+    out[1] = GradIO<GT>::to_f32(b);
+}
+
+template <typename GT, bool NT, int W>
+__device__ __forceinline__ void load_grad(const GT* G, float out[W]) {
+    static_assert(W == 4 || W == 8, "4 or 8 elements per access");
     if constexpr (sizeof(GT) == 4) {
-        const f32x4 x = ld16<NT>(reinterpret_cast<const float*>(G));
-        out[0] = x.x; out[1] = x.y; out[2] = x.z; out[3] = x.w;
-    } else {
-        const u32x2 x = ld8<NT>(G);
-        const uint16_t h[4] = {static_cast<uint16_t>(x.x & 0xFFFFu), static_cast<uint16_t>(x.x >> 16),
-                               static_cast<uint16_t>(x.y & 0xFFFFu), static_cast<uint16_t>(x.y >> 16)};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            GT t;
-            std::memcpy(&t, &h[k], 2);
-            out[k] = GradIO<GT>::to_f32(t);
+        for (int k = 0; k < W / 4; ++k) {
+            const f32x4 x = ld16<NT>(reinterpret_cast<const float*>(G) + 4 * k);
+            out[4 * k] = x.x; out[4 * k + 1] = x.y; out[4 * k + 2] = x.z; out[4 * k + 3] = x.w;
         }
+    } else if constexpr (W == 4) {
+        const u32x2 x = ld8<NT>(G);
+        unpack16<GT>(x.x, out);
+        unpack16<GT>(x.y, out + 2);
+    } else {
+        const f32x4 x = ld16<NT>(reinterpret_cast<const float*>(G));
+        const u32x4 w = __builtin_bit_cast(u32x4, x);
+        unpack16<GT>(w.x, out);
+        unpack16<GT>(w.y, out + 2);
+        unpack16<GT>(w.z, out + 4);
+        unpack16<GT>(w.w, out + 6);
     }
 }
 
@@ -278,17 +297,17 @@ __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
             const int64_t nvec = len / kVec;
             int64_t i = threadIdx.x;
             for (; i + (kNormUnroll - 1) * kBlock < nvec; i += kNormUnroll * kBlock) {
-                float x[kNormUnroll][4];
+                float x[kNormUnroll][kVec];
 #pragma unroll
-                for (int u = 0; u < kNormUnroll; ++u) load_grad4<GT, kNtNormLoad>(g + (i + u * kBlock) * kVec, x[u]);
+                for (int u = 0; u < kNormUnroll; ++u) load_grad<GT, kNtNormLoad, kVec>(g + (i + u * kBlock) * kVec, x[u]);
 #pragma unroll
                 for (int u = 0; u < kNormUnroll; ++u)
 #pragma unroll
                     for (int k = 0; k < kVec; ++k) norm_accum(x[u][k], inv, unscale, acc, bad);
             }
             for (; i < nvec; i += kBlock) {
-                float x[4];
-                load_grad4<GT, kNtNormLoad>(g + i * kVec, x);
+                float x[kVec];
+                load_grad<GT, kNtNormLoad, kVec>(g + i * kVec, x);
 #pragma unroll
                 for (int k = 0; k < kVec; ++k) norm_accum(x[k], inv, unscale, acc, bad);
             }
@@ -415,56 +434,88 @@ template <int LOWP>
 struct LowpStore;
 template <>
 struct LowpStore<MGOPT_NONE> {
-    static __device__ __forceinline__ void store4(void*, const float*) {}
+    template <int W>
+    static __device__ __forceinline__ void store(void*, const float*) {}
     static __device__ __forceinline__ void store1(void*, float) {}
 };
 template <>
 struct LowpStore<MGOPT_BF16> {
-    static __device__ __forceinline__ void store4(void* p, const float* x) {
-        uint2 q;
-        q.x = static_cast<uint32_t>(f32_to_bf16_rne(x[0])) | (static_cast<uint32_t>(f32_to_bf16_rne(x[1])) << 16);
-        q.y = static_cast<uint32_t>(f32_to_bf16_rne(x[2])) | (static_cast<uint32_t>(f32_to_bf16_rne(x[3])) << 16);
-        *reinterpret_cast<uint2*>(p) = q;
+    template <int W>
+    static __device__ __forceinline__ void store(void* p, const float* x) {
+        uint32_t w[W / 2];
+#pragma unroll
+        for (int k = 0; k < W / 2; ++k)
+            w[k] = static_cast<uint32_t>(f32_to_bf16_rne(x[2 * k])) | (static_cast<uint32_t>(f32_to_bf16_rne(x[2 * k + 1])) << 16);
+        if constexpr (W == 4) st8<kNtStore>(p, u32x2{w[0], w[1]});
+        else st16<kNtStore>(static_cast<float*>(p), __builtin_bit_cast(f32x4, u32x4{w[0], w[1], w[2], w[3]}));
     }
     static __device__ __forceinline__ void store1(void* p, float x) { *static_cast<uint16_t*>(p) = f32_to_bf16_rne(x); }
 };
 template <>
 struct LowpStore<MGOPT_F16> {
-    static __device__ __forceinline__ void store4(void* p, const float* x) {
-        Vec4<_Float16> h;
+    template <int W>
+    static __device__ __forceinline__ void store(void* p, const float* x) {
+        uint32_t w[W / 2];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) h.e[k] = static_cast<_Float16>(x[k]);
-        ::store4(static_cast<_Float16*>(p), h);
+        for (int k = 0; k < W / 2; ++k) {
+            const _Float16 a = static_cast<_Float16>(x[2 * k]), b = static_cast<_Float16>(x[2 * k + 1]);
+            uint16_t ha, hb;
+            std::memcpy(&ha, &a, 2);
+            std::memcpy(&hb, &b, 2);
+            w[k] = static_cast<uint32_t>(ha) | (static_cast<uint32_t>(hb) << 16);
+        }
+        if constexpr (W == 4) st8<kNtStore>(p, u32x2{w[0], w[1]});
+        else st16<kNtStore>(static_cast<float*>(p), __builtin_bit_cast(f32x4, u32x4{w[0], w[1], w[2], w[3]}));
     }
     static __device__ __forceinline__ void store1(void* p, float x) { *static_cast<_Float16*>(p) = static_cast<_Float16>(x); }
 };
 
-// Four consecutive elements of one tensor through pass 2: load() issues the
+// kVec consecutive elements of one tensor through pass 2: load() issues the
 // memory reads, finish() does the arithmetic and the writes.
 template <typename GT>
-struct Quad {
-    float g[4];
-    f32x4 p, m, v;
+struct Group {
+    static constexpr int W = kVec;
+    float g[W];
+    f32x4 p[W / 4], m[W / 4], v[W / 4];
 
     __device__ __forceinline__ void load(const GT* G, const float* P, const float* M, const float* V, int64_t e) {
-        load_grad4<GT, kNtLoad>(G + e, g);
-        p = ld16<kNtLoad>(P + e);
-        m = ld16<kNtLoad>(M + e);
-        v = ld16<kNtLoad>(V + e);
+        load_grad<GT, kNtLoad, W>(G + e, g);
+#pragma unroll
+        for (int k = 0; k < W / 4; ++k) {
+            p[k] = ld16<kNtLoad>(P + e + 4 * k);
+            m[k] = ld16<kNtLoad>(M + e + 4 * k);
+            v[k] = ld16<kNtLoad>(V + e + 4 * k);
+        }
     }
 
     template <int LOWP>
     __device__ __forceinline__ void finish(GT* G, float* P, float* M, float* V, void* L, int64_t e, const ElemConst& c,
                                            bool wb) {
-        float pf[4] = {p.x, p.y, p.z, p.w}, mf[4] = {m.x, m.y, m.z, m.w}, vf[4] = {v.x, v.y, v.z, v.w};
-        Vec4<GT> go;
+        float pf[W], mf[W], vf[W], gc[W];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) go.e[k] = GradIO<GT>::from_f32(adam_elem(g[k], pf[k], mf[k], vf[k], c));
-        st16<kNtStore>(P + e, f32x4{pf[0], pf[1], pf[2], pf[3]});
-        st16<kNtStore>(M + e, f32x4{mf[0], mf[1], mf[2], mf[3]});
-        st16<kNtStore>(V + e, f32x4{vf[0], vf[1], vf[2], vf[3]});
-        if constexpr (LOWP != MGOPT_NONE) LowpStore<LOWP>::store4(static_cast<uint16_t*>(L) + e, pf);
-        if (wb) store4(G + e, go);
+        for (int k = 0; k < W / 4; ++k) {
+            pf[4 * k] = p[k].x; pf[4 * k + 1] = p[k].y; pf[4 * k + 2] = p[k].z; pf[4 * k + 3] = p[k].w;
+            mf[4 * k] = m[k].x; mf[4 * k + 1] = m[k].y; mf[4 * k + 2] = m[k].z; mf[4 * k + 3] = m[k].w;
+            vf[4 * k] = v[k].x; vf[4 * k + 1] = v[k].y; vf[4 * k + 2] = v[k].z; vf[4 * k + 3] = v[k].w;
+        }
+#pragma unroll
+        for (int k = 0; k < W; ++k) gc[k] = adam_elem(g[k], pf[k], mf[k], vf[k], c);
+#pragma unroll
+        for (int k = 0; k < W / 4; ++k) {
+            st16<kNtStore>(P + e + 4 * k, f32x4{pf[4 * k], pf[4 * k + 1], pf[4 * k + 2], pf[4 * k + 3]});
+            st16<kNtStore>(M + e + 4 * k, f32x4{mf[4 * k], mf[4 * k + 1], mf[4 * k + 2], mf[4 * k + 3]});
+            st16<kNtStore>(V + e + 4 * k, f32x4{vf[4 * k], vf[4 * k + 1], vf[4 * k + 2], vf[4 * k + 3]});
+        }
+        if constexpr (LOWP != MGOPT_NONE) LowpStore<LOWP>::template store<W>(static_cast<uint16_t*>(L) + e, pf);
+        if (wb) {
+#pragma unroll
+            for (int k = 0; k < W / 4; ++k) {
+                Vec4<GT> go;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) go.e[j] = GradIO<GT>::from_f32(gc[4 * k + j]);
+                store4(G + e + 4 * k, go);
+            }
+        }
     }
 };
 
@@ -513,21 +564,21 @@ __global__ void __launch_bounds__(kBlock) adamw_kernel(const AdamArgs a) {
 
     int64_t done = 0;
     const bool vec = aligned(P, 16) && aligned(M, 16) && aligned(V, 16) && aligned(g, sizeof(GT) * kVec) &&
-                     (LOWP == MGOPT_NONE || aligned(L, 8));
+                     (LOWP == MGOPT_NONE || aligned(L, 2 * kVec));
     if (vec) {
         // four elements per thread per access; kUnroll accesses issued before
         // the first one is consumed, to keep more bytes in flight per wave
         const int64_t nvec = len / kVec;
         int64_t i = threadIdx.x;
         for (; i + (kUnroll - 1) * kBlock < nvec; i += kUnroll * kBlock) {
-            Quad<GT> q[kUnroll];
+            Group<GT> q[kUnroll];
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) q[u].load(g, P, M, V, (i + u * kBlock) * kVec);
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) q[u].template finish<LOWP>(g, P, M, V, L, (i + u * kBlock) * kVec, c, wb);
         }
         for (; i < nvec; i += kBlock) {
-            Quad<GT> q;
+            Group<GT> q;
             q.load(g, P, M, V, i * kVec);
             q.template finish<LOWP>(g, P, M, V, L, i * kVec, c, wb);
         }
