@@ -117,6 +117,27 @@ def lib() -> ctypes.CDLL:
     return load_library()
 
 
+HOST_PATH = Path(__file__).resolve().parent / "_build" / "host" / "mgopt_host.so"
+_host = None
+
+
+def host():
+    """The host-side helper module (per-step pointer gathering in C++)."""
+    global _host
+    if _host is None:
+        import importlib.util
+
+        import torch  # noqa: F401  (loads the libtorch libraries the helper links against)
+
+        if not HOST_PATH.exists():
+            raise RuntimeError(f"{HOST_PATH} is not built; run __graft_entry__.build()")
+        spec = importlib.util.spec_from_file_location("mgopt_host", HOST_PATH)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _host = mod
+    return _host
+
+
 def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = load_library().mgopt_last_error().decode(errors="replace")

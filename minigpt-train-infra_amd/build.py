@@ -56,5 +56,22 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+HOST_SRC = HERE / "csrc" / "host_ptrs.cpp"
+HOST_DIR = OUT_DIR / "host"
+
+
+def build_host(verbose: bool = False) -> Path:
+    """Builds the host-side helper (a torch C++ extension) into _build/host/."""
+    from torch.utils.cpp_extension import load
+
+    if HOST_DIR.exists():
+        shutil.rmtree(HOST_DIR)
+    HOST_DIR.mkdir(parents=True)
+    load(name="mgopt_host", sources=[str(HOST_SRC)], build_directory=str(HOST_DIR), extra_cflags=["-O2"],
+         verbose=verbose)
+    return HOST_DIR / "mgopt_host.so"
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
+    print(build_host(verbose=False))

@@ -23,6 +23,7 @@ import ctypes
 import math
 from typing import Any, Sequence
 
+import numpy as np
 import torch
 
 from . import _native as N
@@ -121,10 +122,13 @@ class _Engine:
                 v["master_param"] = self.master[mo : mo + n].view(p.shape)
             self.views.append(v)
 
-        self.param_ptrs = [p.data_ptr() for p in self.params]
+        self.param_ptr_bytes = np.array([p.data_ptr() for p in self.params], np.int64).tobytes()
+        self.param_dtype_codes = tuple(N.dtype_code(p.dtype) for p in self.params)
+        self.pset = None
         self.plan: int | None = None
         self.plan_grad_dtypes: tuple[int, ...] | None = None
-        self.grad_ptrs: list[int] | None = None
+        self.grad_ptr_bytes: bytes | None = None
+        self.grad_dtype_bytes: bytes | None = None
         self.grad_source: list[torch.Tensor | None] | None = None
         self.grad_source_checked = False
         self.complete_keys: set[tuple[int, ...]] = set()   # id tuples of parameter lists equal to self.params
@@ -180,7 +184,7 @@ class _Engine:
             )
         self.plan = plan.value
         self.plan_grad_dtypes = grad_dtypes
-        self.grad_ptrs = None
+        self.grad_ptr_bytes = None
 
     def set_grad_source(self, grads: Sequence[torch.Tensor | None] | None) -> None:
         if grads is not None:
@@ -192,6 +196,7 @@ class _Engine:
                     raise ValueError("gradient shape does not match its parameter")
         self.grad_source = grads
         self.grad_source_checked = False
+        self.pset = None
 
     def current_grads(self) -> list[torch.Tensor | None]:
         if self.grad_source is not None:
@@ -206,48 +211,53 @@ class _Engine:
         self._prepare()
         self.prepared = True
 
+    def _param_set(self):
+        if self.pset is None:
+            self.pset = N.host().ParamSet(self.params, [] if self.grad_source is None else self.grad_source)
+        return self.pset
+
     def _prepare(self) -> None:
-        ptrs = [p.data_ptr() for p in self.params]
-        if ptrs != self.param_ptrs:
-            raise RuntimeError(
-                "a parameter's storage moved (param.data was replaced) after the optimizer was built; "
-                "copy new values in place with param.data.copy_() instead"
-            )
-        # a gradient source given with set_grad_source is a fixed set of
-        # tensors: validated and uploaded once
+        ps = self._param_set()
         if self.grad_source is not None and self.grad_source_checked and self.plan is not None:
+            # a fixed gradient source is validated and uploaded once; only the
+            # parameters' storage is re-checked
+            if ps.param_ptrs() != self.param_ptr_bytes:
+                self._moved()
             return
-        grads = self.current_grads()
-        gptrs = [0 if g is None else g.data_ptr() for g in grads]
-        if gptrs == self.grad_ptrs and self.plan is not None:
+        pptrs, gptrs, gdt, gflags = ps.gather()
+        if pptrs != self.param_ptr_bytes:
+            self._moved()
+        if gptrs == self.grad_ptr_bytes and gdt == self.grad_dtype_bytes and self.plan is not None:
             return
-        dtypes = []
-        for g, p in zip(grads, self.params):
-            if g is None:
-                dtypes.append(N.dtype_code(p.dtype))
-                continue
-            if g.is_sparse:
-                raise RuntimeError("mgopt AdamW does not support sparse gradients")
-            if g.device != self.device:
-                raise RuntimeError("gradient on a different device than its parameter")
-            if not g.is_contiguous():
-                raise RuntimeError("mgopt AdamW needs contiguous gradients")
-            if g.numel() != p.numel():
-                raise RuntimeError("gradient size does not match its parameter")
-            dtypes.append(N.dtype_code(g.dtype))
-        dtypes_t = tuple(dtypes)
+        flags = np.frombuffer(gflags, np.int8)
+        if flags.any():
+            i = int(np.flatnonzero(flags)[0])
+            f = int(flags[i])
+            what = ("is sparse" if f & 8 else "lives on another device" if f & 4 else
+                    "has a different size than its parameter" if f & 2 else "is not contiguous")
+            raise RuntimeError(f"gradient of parameter {i} {what}; mgopt AdamW needs dense contiguous "
+                               "gradients on the parameters' GPU")
+        codes = np.frombuffer(gdt, np.int8)
+        if (codes == -2).any():
+            i = int(np.flatnonzero(codes == -2)[0])
+            raise TypeError(f"gradient of parameter {i} has an unsupported dtype; expected float32, float16 or bfloat16")
+        # a tensor without a grad this step keeps the dtype it had (or its parameter's)
+        prev = self.plan_grad_dtypes if self.plan_grad_dtypes is not None else self.param_dtype_codes
+        dtypes_t = tuple(prev[i] if c < 0 else int(c) for i, c in enumerate(codes))
         if self.plan is None or dtypes_t != self.plan_grad_dtypes:
-            # tensors without a grad this step keep the dtype of the previous plan
-            if self.plan_grad_dtypes is not None:
-                dtypes_t = tuple(self.plan_grad_dtypes[i] if grads[i] is None else dtypes_t[i] for i in range(len(grads)))
-            if self.plan is None or dtypes_t != self.plan_grad_dtypes:
-                self._build_plan(dtypes_t)
-        arr = (ctypes.c_void_p * len(gptrs))(*[p or None for p in gptrs])
+            self._build_plan(dtypes_t)
+        arr = ctypes.cast(ctypes.c_char_p(gptrs), ctypes.POINTER(ctypes.c_void_p))
         N.check(N.lib().mgopt_plan_set_grads(ctypes.c_void_p(self.plan), arr, ctypes.c_void_p(N.stream_handle(self.device))),
                 "mgopt_plan_set_grads")
-        self.grad_ptrs = gptrs
+        self.grad_ptr_bytes, self.grad_dtype_bytes = gptrs, gdt
         if self.grad_source is not None:
             self.grad_source_checked = True
+
+    def _moved(self) -> None:
+        raise RuntimeError(
+            "a parameter's storage moved (param.data was replaced) after the optimizer was built; "
+            "copy new values in place with param.data.copy_() instead"
+        )
 
     # ------------------------------------------------------- iteration state
     def reset_iteration(self) -> None:
