@@ -150,6 +150,15 @@ MGOPT_API int mgopt_scale_grads(mgopt_plan* plan, const float* coef_dev, void* s
 /* Copies every lowp parameter into its fp32 master (exact widening). */
 MGOPT_API int mgopt_sync_master(mgopt_plan* plan, void* stream);
 
+/* Registers a caller-owned 16-byte device buffer (NULL: none) that later
+ * calls keep log-window statistics in: float last norm, float running maximum
+ * of norms (NaN propagates, as torch.maximum does), uint32 skipped steps,
+ * uint32 taken steps.  mgopt_grad_norm updates the norms when it writes a norm;
+ * mgopt_adamw_step counts the step.  Replaces the per-step
+ * torch.maximum(window_grad_norm_max, grad_norm) and the optimizer-step /
+ * skip bookkeeping of train.py:487-489,501-507. */
+MGOPT_API int mgopt_plan_set_window(mgopt_plan* plan, void* window_dev);
+
 /* Blocking read of the plan's device error flag: nonzero when a pass-2
  * work-group met a step count outside the bias-correction table and left its
  * tensor untouched.  No reference counterpart (a safety net of this engine). */

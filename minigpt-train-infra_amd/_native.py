@@ -28,6 +28,7 @@ EXPORTS = (
     "mgopt_scaler_update",
     "mgopt_scale_grads",
     "mgopt_sync_master",
+    "mgopt_plan_set_window",
     "mgopt_plan_error_flag",
     "mgopt_synth_fill",
     "mgopt_last_error",
@@ -81,6 +82,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "mgopt_scaler_update": (ctypes.c_int, [vp, vp, ctypes.POINTER(vp), i32, dbl, dbl, i32, vp]),
         "mgopt_scale_grads": (ctypes.c_int, [vp, vp, vp]),
         "mgopt_sync_master": (ctypes.c_int, [vp, vp]),
+        "mgopt_plan_set_window": (ctypes.c_int, [vp, vp]),
         "mgopt_plan_error_flag": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_int)]),
         "mgopt_synth_fill": (ctypes.c_int, [vp, i32, i64, u64, u64, dbl, u64, dbl, vp]),
         "mgopt_last_error": (ctypes.c_char_p, []),

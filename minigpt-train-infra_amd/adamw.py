@@ -232,15 +232,63 @@ class AdamW(torch.optim.Optimizer):
         return loss
 
     def zero_grad(self, set_to_none: bool = True) -> None:
-        super().zero_grad(set_to_none=set_to_none)
+        arena = getattr(self, "_grad_arena", None)
+        if arena is not None:
+            # the arena persists: one fill, and every p.grad is (again) its view
+            arena.zero_()
+            for p, g in zip(self._get_engine().params, self._grad_views):
+                if p.grad is not g:
+                    p.grad = g
+        else:
+            super().zero_grad(set_to_none=set_to_none)
         if self._engine is not None:
             self._engine.reset_iteration()
+
+    def use_grad_arena(self, dtype: torch.dtype | None = None) -> torch.Tensor:
+        """Backs every parameter's .grad with a view of one flat device buffer
+        (segments on 256-byte boundaries, the layout of the moment arenas), so
+        gradients are contiguous across the whole parameter set and
+        zero_grad() is a single fill whatever set_to_none says; autograd then
+        accumulates into the views in place.  dtype: gradient dtype when it
+        differs from the parameters' (fp16 gradients for fp32 parameters, for
+        instance; sets each parameter's grad_dtype).  Returns the buffer."""
+        eng = self._get_engine()
+        dts = {p.dtype for p in eng.params}
+        if dtype is None:
+            if len(dts) != 1:
+                raise ValueError("parameters of several dtypes: pass the gradient dtype explicitly")
+            dtype = next(iter(dts))
+        if dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            raise TypeError(f"unsupported gradient dtype {dtype}")
+        arena = torch.zeros(max(eng.total, 1), dtype=dtype, device=eng.device)
+        views = []
+        for p, off in zip(eng.params, eng.offsets):
+            if dtype != p.dtype:
+                p.grad_dtype = dtype
+            views.append(arena[off : off + p.numel()].view(p.shape))
+        with torch.no_grad():
+            for p, g in zip(eng.params, views):
+                if p.grad is not None:
+                    g.copy_(p.grad)
+                p.grad = g
+        self._grad_arena = arena
+        self._grad_views = views
+        eng.reset_iteration()
+        return arena
 
     def set_grad_source(self, grads: Iterable[torch.Tensor | None] | None) -> None:
         """Reads gradients from these tensors (one per parameter, in
         param_groups order; fp32, fp16 or bf16) instead of p.grad.  None
         restores p.grad."""
         self._get_engine().set_grad_source(None if grads is None else list(grads))
+
+    def window_metrics(self, reset: bool = True) -> dict:
+        """Statistics accumulated on the GPU since the last reset, read with one
+        copy: last and maximum clip_grad_norm_ result (maximum with
+        torch.maximum's NaN rule, from 0), optimizer steps skipped on inf/NaN and
+        taken.  Replaces the per-step window bookkeeping of train.py:487-489 and
+        the optimizer-step difference of train.py:501-507."""
+        return self._get_engine().window_metrics(reset)
 
     def sync_master_from_params(self) -> None:
         """Re-reads bf16/fp16 parameters into the fp32 master copy (after the

@@ -64,6 +64,15 @@ struct Partial {
     uint32_t pad;
 };
 
+// Log-window statistics kept on the device so a training loop reads them once
+// per window (train.py:434-441,487-489,501-507) instead of syncing per step.
+struct Window {
+    float norm_last;   // last clip_grad_norm_ result
+    float norm_max;    // running maximum, torch.maximum semantics (NaN propagates)
+    uint32_t skipped;  // optimizer steps skipped on found_inf
+    uint32_t taken;    // optimizer steps taken
+};
+
 struct GroupConst {
     double lr, wd, beta1, beta2, eps;
     int32_t maximize;
@@ -331,7 +340,7 @@ __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
 
 __global__ void __launch_bounds__(kFinalizeBlock)
     finalize_kernel(const Partial* partials, int64_t n, double max_norm, float* norm_out, float* coef_out,
-                    float* found_inf_out) {
+                    float* found_inf_out, Window* win) {
     double s = 0.0;
     uint32_t f = 0;
     for (int64_t i = threadIdx.x; i < n; i += kFinalizeBlock) {
@@ -348,6 +357,11 @@ __global__ void __launch_bounds__(kFinalizeBlock)
     else if (isinf(static_cast<float>(s))) norm = __builtin_inff();
     else norm = static_cast<float>(sqrt(s));
     if (norm_out) *norm_out = norm;
+    if (norm_out && win) {
+        win->norm_last = norm;
+        const float m = win->norm_max;
+        win->norm_max = (isnan(m) || isnan(norm)) ? __builtin_nanf("") : fmaxf(m, norm);
+    }
     if (coef_out) {
         // clip_grad.py:165-169 -> reciprocal(norm + 1e-6) * max_norm, clamp(max=1);
         // NaN propagates through the clamp
@@ -369,10 +383,14 @@ __global__ void __launch_bounds__(kFinalizeBlock)
 // subtracts found_inf back (adam.py:877-899).  Tensors without grad keep their
 // count (adam.py:153).
 __global__ void __launch_bounds__(kBlock)
-    prologue_kernel(const void* const* grads, float* steps, int32_t n, const float* found_inf) {
+    prologue_kernel(const void* const* grads, float* steps, int32_t n, const float* found_inf, Window* win) {
     const int32_t i = blockIdx.x * kBlock + threadIdx.x;
-    if (i >= n) return;
-    if (found_inf != nullptr && *found_inf != 0.0f) return;
+    const bool skip = found_inf != nullptr && *found_inf != 0.0f;
+    if (win && i == 0) {
+        if (skip) win->skipped += 1u;
+        else win->taken += 1u;
+    }
+    if (i >= n || skip) return;
     if (grads[i] != nullptr) steps[i] = steps[i] + 1.0f;
 }
 
@@ -728,6 +746,7 @@ struct mgopt_plan {
     Partial* d_partials = nullptr;
     int* d_err = nullptr;
     float* d_steps = nullptr;
+    Window* d_window = nullptr;  // caller-owned, optional
     struct Class {
         int32_t grad_dtype;
         int32_t lowp_dtype;
@@ -946,7 +965,7 @@ MGOPT_API int mgopt_grad_norm(mgopt_plan* P, const float* scale_dev, double max_
         if (rc) return rc;
     }
     hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(kFinalizeBlock), 0, s, P->d_partials, P->n_chunks, max_norm, norm_dev,
-                       coef_dev, found_inf_dev);
+                       coef_dev, found_inf_dev, P->d_window);
     return launch_check("finalize_kernel");
 }
 
@@ -961,7 +980,7 @@ MGOPT_API int mgopt_adamw_step(mgopt_plan* P, const mgopt_group_hparams* groups,
     hipStream_t s = static_cast<hipStream_t>(stream);
 
     hipLaunchKernelGGL(prologue_kernel, dim3((P->n_tensors + kBlock - 1) / kBlock), dim3(kBlock), 0, s,
-                       const_cast<const void* const*>(P->d_grads), P->d_steps, P->n_tensors, found_inf_dev);
+                       const_cast<const void* const*>(P->d_grads), P->d_steps, P->n_tensors, found_inf_dev, P->d_window);
     if (int rc = launch_check("prologue_kernel")) return rc;
 
     AdamArgs a;
@@ -1059,6 +1078,13 @@ MGOPT_API int mgopt_sync_master(mgopt_plan* P, void* stream) {
             continue;
         if (int rc = launch_check("sync_master_kernel")) return rc;
     }
+    return 0;
+}
+
+MGOPT_API int mgopt_plan_set_window(mgopt_plan* P, void* window_dev) {
+    if (!P) return fail(MGOPT_E_INVALID, "NULL plan");
+    if (reinterpret_cast<uintptr_t>(window_dev) % 4 != 0) return fail(MGOPT_E_ALIGN, "window buffer must be 4-byte aligned");
+    P->d_window = static_cast<Window*>(window_dev);
     return 0;
 }
 

@@ -106,6 +106,8 @@ class _Engine:
             self.steps = torch.zeros(len(self.params), dtype=torch.float32, device=dev)
             self.found_inf = torch.zeros((), dtype=torch.float32, device=dev)
             self.coef = torch.ones((), dtype=torch.float32, device=dev)
+            # log-window record: norm_last, norm_max (fp32), skipped, taken (uint32)
+            self.window = torch.zeros(4, dtype=torch.float32, device=dev)
         self.master_synced = not self.has_master
 
         # views handed out through optimizer.state
@@ -183,6 +185,8 @@ class _Engine:
                 "mgopt_plan_create",
             )
         self.plan = plan.value
+        N.check(lib.mgopt_plan_set_window(ctypes.c_void_p(self.plan), ctypes.c_void_p(self.window.data_ptr())),
+                "mgopt_plan_set_window")
         self.plan_grad_dtypes = grad_dtypes
         self.grad_ptr_bytes = None
 
@@ -370,6 +374,20 @@ class _Engine:
             "mgopt_adamw_step",
         )
         self.reset_iteration()
+
+    def window_metrics(self, reset: bool = True) -> dict:
+        """Reads the log-window record (one device-to-host copy)."""
+        w = self.window.detach().cpu()
+        counts = w.view(torch.int32)
+        out = {
+            "grad_norm_last": float(w[0]),
+            "grad_norm_max": float(w[1]),
+            "skipped_steps": int(counts[2]),
+            "optimizer_steps": int(counts[3]),
+        }
+        if reset:
+            self.window.zero_()
+        return out
 
     def error_flag(self) -> int:
         out = ctypes.c_int(0)

@@ -305,3 +305,64 @@ def test_scaler_stage_errors_match_torch():
         sc.update()
     st = sc.state_dict()
     assert set(st) == {"scale", "growth_factor", "backoff_factor", "growth_interval", "_growth_tracker"}
+
+
+def test_window_metrics_replace_per_step_bookkeeping():
+    """The device window record equals what train.py:487-489,501-507 computes
+    with torch.maximum and optimizer-step differences."""
+    params = _params([(300, 7), (33,)])
+    opt = mg.AdamW(params, lr=1e-3)
+    sc = mg.GradScaler("cuda", init_scale=256.0)
+    sc.scale(torch.ones((), device=DEV))
+    norms = []
+    for s in range(1, 8):
+        _grads(params, s, 0.3 * sc.get_scale())
+        if s == 3:
+            params[0].grad.view(-1)[5] = float("inf")
+        sc.unscale_(opt)
+        norms.append(mg.clip_grad_norm_(params, 1.0))
+        sc.step(opt)
+        sc.update()
+    w = opt.window_metrics()
+    ref_max = torch.zeros((), device=DEV)
+    for n in norms:
+        ref_max = torch.maximum(ref_max, n.detach().float())
+    assert w["grad_norm_last"] == float(norms[-1])
+    assert w["grad_norm_max"] == float(ref_max) == float("inf")
+    assert w["skipped_steps"] == 1 and w["optimizer_steps"] == 6
+    assert mg.optimizer_completed_steps(opt) == 6
+    assert opt.window_metrics() == {"grad_norm_last": 0.0, "grad_norm_max": 0.0, "skipped_steps": 0, "optimizer_steps": 0}
+
+
+def test_grad_arena_matches_fresh_gradients():
+    """Backward into an arena (zero_grad = one fill, autograd accumulates in
+    place, two micro-batches as in train.py:467-481) gives the same training
+    trajectory as fresh gradients every step."""
+    def model():
+        torch.manual_seed(0)
+        return torch.nn.Sequential(torch.nn.Linear(64, 256), torch.nn.GELU(), torch.nn.Linear(256, 10)).to(DEV)
+
+    runs = []
+    for arena in (False, True):
+        net = model()
+        opt = mg.AdamW(mg.build_adamw_param_groups(net, 0.1), lr=1e-3, betas=(0.9, 0.95))
+        if arena:
+            buf = opt.use_grad_arena()
+            assert all(p.grad.untyped_storage().data_ptr() == buf.untyped_storage().data_ptr() for p in net.parameters())
+        gen = torch.Generator(device=DEV).manual_seed(1)
+        norms = []
+        for s in range(6):
+            mg.set_optimizer_lr(opt, mg.cosine_lr(s, 1e-3, 1e-4, 2, 6))
+            opt.zero_grad(set_to_none=True)
+            for _ in range(2):
+                x = torch.randn(32, 64, device=DEV, generator=gen)
+                y = torch.randint(0, 10, (32,), device=DEV, generator=gen)
+                (torch.nn.functional.cross_entropy(net(x), y) / 2).backward()
+            norms.append(float(mg.clip_grad_norm_(net.parameters(), 0.5)))
+            opt.step()
+        torch.cuda.synchronize()
+        runs.append(([p.detach().clone() for p in net.parameters()], norms))
+    (pa, na), (pb, nb) = runs
+    assert na == nb
+    for x, y in zip(pa, pb):
+        assert torch.equal(x, y)
