@@ -99,9 +99,14 @@ class Pair:
         if self.separate:
             self.grads = [torch.empty(s, dtype=DTYPES[case.grad_dtype], device=dev) for _, s in self.shapes]
             self.opt.set_grad_source(self.grads)
-        # oracle
+        # oracle: initial values of the tensors whose update it computes (all
+        # of them unless a subset is given; the others are empty placeholders)
         init = []
+        keep = set(range(len(self.shapes))) if case.subset is None else set(case.subset)
         for i, (_, shape) in enumerate(self.shapes):
+            if i not in keep:
+                init.append(np.zeros(0, np.float32))
+                continue
             n = int(np.prod(shape)) if shape else 1
             x = O.synth(n, syn.PARAM_SEED, syn.param_stream(i), O.synth_k(0.02))
             init.append(O.round_to(x, case.param_dtype))

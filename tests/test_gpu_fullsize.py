@@ -1,0 +1,146 @@
+"""GPU parity at the full sizes of the workloads the step is specified on.
+
+At these sizes the oracle computes the gradient norm and the skip decision from
+every gradient (copied to the host each step), and the AdamW update of a subset
+of tensors (every no-decay tensor plus a few matrices of each kind); the rest of
+the state is checked through size-independent properties on the device: the
+bf16 model copy is the round-to-nearest-even image of the master everywhere,
+a skipped step leaves every arena bit for bit unchanged (integer checksums of
+the bit patterns), and every step count equals the number of steps taken.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from tests._compare import ULP_LOWP, exact_fraction, rel, ulp16, RTOL_NORM
+from tests._gpu_harness import Case, Pair, log, mg
+
+pytestmark = pytest.mark.gpu
+
+
+def _checksums(pair: Pair) -> list[int]:
+    eng = pair.opt._engine
+    arenas = [eng.exp_avg, eng.exp_avg_sq] + ([eng.master] if eng.master is not None else [])
+    if eng.master is None:
+        arenas += [p.detach() for p in pair.params]
+    return [int(a.reshape(-1).view(torch.int32).sum()) for a in arenas]
+
+
+def _check_full(pair: Pair, label: str, expect_steps: int) -> None:
+    """Norms, skips and the oracle subset bit for bit; the rest by properties."""
+    norms = [float(t) for t in pair.norms_gpu]
+    for s, (ng, out) in enumerate(zip(norms, pair.outs)):
+        no = out["norm"]
+        if math.isfinite(no):
+            assert rel(ng, no) <= RTOL_NORM, (label, s + 1, ng, no)
+        else:
+            assert (math.isnan(no) and math.isnan(ng)) or ng == no, (label, s + 1, ng, no)
+    exact_norms = sum(1 for ng, out in zip(norms, pair.outs) if ng == out["norm"] or not math.isfinite(out["norm"]))
+    if pair.case.scaler:
+        assert [float(t) for t in pair.scale_gpu] == [o["scale"] for o in pair.outs]
+    for i in pair.case.subset:
+        st = pair.gpu_state(i)
+        assert st["step"] == pair.orc.steps[i] == expect_steps
+        for k, ref in (("p", pair.orc.p[i]), ("m", pair.orc.m[i]), ("v", pair.orc.v[i])):
+            assert exact_fraction(st[k], ref.ravel()) == 1.0, (label, k, i)
+        if "lowp_bits" in st:
+            assert ulp16(st["lowp_bits"], pair.oracle_lowp_bits(i)) <= ULP_LOWP
+    eng = pair.opt._engine
+    assert bool((eng.steps == float(expect_steps)).all())
+    if eng.master is not None:
+        for i, p in enumerate(pair.params):
+            m = pair.opt.state[p]["master_param"]
+            assert torch.equal(m.to(p.dtype).view(torch.int16), p.detach().view(torch.int16)), (label, i)
+    assert eng.error_flag() == 0
+    log(f"[{label}] {len(norms)} steps, norms exact {exact_norms}/{len(norms)}, "
+        f"subset of {len(pair.case.subset)} tensors bit-exact")
+
+
+def _run_with_skip_check(pair: Pair, steps: int, skip_step: int) -> None:
+    c = pair.case
+    for s in range(1, steps + 1):
+        lr = mg.cosine_lr(s - 1, *c.lr_sched)
+        mg.set_optimizer_lr(pair.opt, lr)
+        pair.fill_grads(s)
+        pair.oracle_step(s, lr)
+        before = _checksums(pair) if s == skip_step else None
+        pair.gpu_step()
+        if before is not None:
+            torch.cuda.synchronize()
+            assert pair.outs[-1]["skipped"]
+            assert _checksums(pair) == before, "a skipped step changed the optimizer state"
+    torch.cuda.synchronize()
+
+
+def test_gpt2_small_200_steps():
+    """GPT-2-small shapes, 124,475,904 fp32 params, fp16 grads N(0,1e-2) x scale,
+    GradScaler 65536 / x2 per 2000 / x0.5, +inf at one seeded element at steps
+    17 and 53, 200 steps."""
+    shapes = mg.paramsets.WORKLOADS["gpt2_small"]()
+    rng = np.random.RandomState(17)
+    inject = {s: [(int(rng.randint(len(shapes))), 0, float("inf"))] for s in (17, 53)}
+    decay_n = sum(1 for _, s in shapes if len(s) >= 2)
+    subset = [1, 4, 5] + list(range(decay_n, len(shapes)))
+    log("case: gpt2_small 200 steps")
+    pair = Pair(Case(shapes=shapes, grad_dtype="f16", steps=200, sigma=1e-2,
+                     scaler=dict(init_scale=65536.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=2000),
+                     inject=inject, subset=subset, lr_sched=(6e-4, 6e-5, 10, 200)))
+    pair.run()
+    assert [s + 1 for s, o in enumerate(pair.outs) if o["skipped"]] == [17, 53]
+    assert pair.outs[-1]["scale"] == 16384.0 and pair.outs[-1]["tracker"] == 200 - 53
+    _check_full(pair, "gpt2_small_200", 198)
+
+
+def test_gpt_1p3b_full_size_bf16_master():
+    """1.3B GPT (24 layers, width 2048, vocab 50304): bf16 params and grads,
+    fp32 master/m/v, grads N(0,1e-3) with 0.1% x100 so clipping acts every
+    step; 20 steps."""
+    shapes = mg.paramsets.WORKLOADS["gpt_1p3b"]()
+    log("case: gpt_1p3b full size, 20 steps")
+    decay = [s for _, s in shapes if len(s) >= 2]
+    nodecay_idx = list(range(len(decay), len(shapes)))
+    subset = [1, 2, 3, len(decay) - 1] + nodecay_idx
+    pair = Pair(Case(shapes=shapes, param_dtype="bf16", grad_dtype="bf16", steps=20, sigma=1e-3,
+                     tail=(1000, 100.0), subset=subset))
+    pair.run()
+    assert all(o["norm"] > 1.0 for o in pair.outs)
+    _check_full(pair, "gpt_1p3b", 20)
+
+
+def test_qwen3_8b_full_size():
+    """Qwen3-8B-shaped set, 8,190,735,360 params (131 GB resident): bf16 params
+    and grads, fp32 master/m/v, GradScaler, clip 1.0; 4 steps with +inf at
+    step 2 (a skipped step over the whole set)."""
+    shapes = mg.paramsets.WORKLOADS["qwen3_8b"]()
+    decay_n = sum(1 for _, s in shapes if len(s) >= 2)
+    subset = [1, 2, 5, decay_n - 2] + list(range(decay_n, len(shapes)))
+    log("case: qwen3_8b full size, 4 steps, inf at step 2")
+    pair = Pair(Case(shapes=shapes, param_dtype="bf16", grad_dtype="bf16", steps=4, sigma=1e-3,
+                     scaler=dict(init_scale=65536.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=2000),
+                     inject={2: [(7, 123, float("inf"))]}, subset=subset, fresh_grads=False))
+    _run_with_skip_check(pair, 4, skip_step=2)
+    assert [o["skipped"] for o in pair.outs] == [False, True, False, False]
+    _check_full(pair, "qwen3_8b", 3)
+
+
+def test_ragged_full_size():
+    """20,000 tensors, log-uniform sizes 1..4M elements, 2.5B elements, fp32
+    params, fp16 grads, GradScaler growth interval 50; 6 steps with a NaN at
+    step 3."""
+    shapes = mg.paramsets.WORKLOADS["ragged_20k"]()
+    log("case: ragged_20k full size, 6 steps, NaN at step 3")
+    # a spread of sizes: the 20 largest, 20 smallest and 20 in the middle (param_groups order)
+    probe_sizes = [(i, math.prod(s)) for i, (_, s) in enumerate([x for x in shapes if len(x[1]) >= 2] +
+                                                                  [x for x in shapes if len(x[1]) < 2])]
+    by_size = sorted(probe_sizes, key=lambda t: t[1])
+    subset = sorted({i for i, _ in by_size[:20] + by_size[-20:] + by_size[len(by_size) // 2 - 10: len(by_size) // 2 + 10]})
+    pair = Pair(Case(shapes=shapes, grad_dtype="f16", steps=6, sigma=1e-2,
+                     scaler=dict(init_scale=65536.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=50),
+                     inject={3: [(by_size[-1][0], 5, float("nan"))]}, subset=subset, fresh_grads=False))
+    _run_with_skip_check(pair, 6, skip_step=3)
+    _check_full(pair, "ragged_20k", 5)
