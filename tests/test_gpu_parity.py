@@ -21,6 +21,7 @@ from tests._gpu_harness import Case, Pair, log, mg, syn
 
 pytestmark = pytest.mark.gpu
 
+
 def check_pair(pair: Pair, indices=None, expect_exact=True, label=""):
     """Compares norms, scale trajectory, step counts and final state."""
     c = pair.case

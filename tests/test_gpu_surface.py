@@ -366,3 +366,79 @@ def test_grad_arena_matches_fresh_gradients():
     assert na == nb
     for x, y in zip(pa, pb):
         assert torch.equal(x, y)
+
+
+def test_fp16_params_and_mixed_dtype_classes():
+    """One optimizer holding fp32 params with fp32 / fp16 / bf16 grads and
+    fp16 and bf16 params with fp32 masters: every (grad dtype, param kind)
+    class is its own kernel instance; all must match the oracle bit for bit."""
+    specs = [  # (shape, param dtype, grad dtype)
+        ((300, 5), torch.float32, torch.float32),
+        ((1001,), torch.float32, torch.float16),
+        ((64, 33), torch.float32, torch.bfloat16),
+        ((5000,), torch.float16, torch.float16),
+        ((77, 13), torch.bfloat16, torch.bfloat16),
+        ((4099,), torch.float16, torch.float32),
+    ]
+    params = []
+    for i, (s, pdt, _) in enumerate(specs):
+        p = torch.empty(s, dtype=pdt, device=DEV)
+        syn.fill_(p, syn.PARAM_SEED, i, 0.02)
+        params.append(torch.nn.Parameter(p))
+    opt = mg.AdamW([{"params": params[:3], "weight_decay": 0.1}, {"params": params[3:], "weight_decay": 0.05}],
+                   lr=1e-3, betas=(0.9, 0.95))
+    grads = [torch.empty(s, dtype=gdt, device=DEV) for s, _, gdt in specs]
+    opt.set_grad_source(grads)
+    sc = mg.GradScaler("cuda", init_scale=1024.0, growth_interval=3)
+    sc.scale(torch.ones((), device=DEV))
+    init = [p.detach().float().cpu().numpy().ravel() for p in params]
+    orc = O.OracleRun(init, [0, 0, 0, 1, 1, 1], [dict(betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1),
+                                                 dict(betas=(0.9, 0.95), eps=1e-8, weight_decay=0.05)],
+                      scaler=dict(init_scale=1024.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=3),
+                      max_norm=1.0)
+    for s in range(1, 9):
+        for i, g in enumerate(grads):
+            syn.fill_(g, syn.GRAD_SEED, syn.grad_stream(s, i), 1e-2 * orc.scale)
+        if s == 4:
+            grads[3].view(-1)[10] = float("inf")
+        host = [to_f32(*host_grad(g)) for g in grads]
+        out = orc.step(host, 1e-3)
+        sc.unscale_(opt)
+        norm = mg.clip_grad_norm_(params, 1.0)
+        sc.step(opt)
+        sc.update()
+        assert float(norm) == out["norm"] or (out["norm"] == float("inf") and float(norm) == float("inf"))
+        assert sc.get_scale() == out["scale"]
+    torch.cuda.synchronize()
+    for i, p in enumerate(params):
+        st = opt.state[p]
+        master = st.get("master_param", p).detach().float().cpu().numpy().ravel()
+        assert exact_fraction(master, orc.p[i]) == 1.0, i
+        assert exact_fraction(st["exp_avg"].cpu().numpy().ravel(), orc.m[i]) == 1.0, i
+        assert exact_fraction(st["exp_avg_sq"].cpu().numpy().ravel(), orc.v[i]) == 1.0, i
+        if p.dtype != torch.float32:
+            bits = p.detach().view(torch.int16).cpu().numpy().view(np.uint16).ravel()
+            ref = O.to_f16(orc.p[i]) if p.dtype == torch.float16 else O.to_bf16(orc.p[i])
+            assert np.array_equal(bits, ref), i
+
+
+def test_one_scaler_two_optimizers():
+    """GradScaler.update sums the found_inf of every optimizer stepped this
+    iteration (grad_scaler.py:517-527): an inf in either one backs off."""
+    pa, pb = _params([(100, 3)]), _params([(57,)])
+    oa, ob = mg.AdamW(pa, lr=1e-3), mg.AdamW(pb, lr=1e-3)
+    sc = mg.GradScaler("cuda", init_scale=64.0, growth_interval=2)
+    sc.scale(torch.ones((), device=DEV))
+    traj = []
+    for s in range(1, 7):
+        _grads(pa, s, 0.1)
+        _grads(pb, s + 100, 0.1)
+        if s == 3:
+            pb[0].grad[0] = float("nan")
+        for o in (oa, ob):
+            sc.unscale_(o)
+            sc.step(o)
+        sc.update()
+        traj.append(sc.get_scale())
+    assert traj == [64.0, 128.0, 64.0, 64.0, 128.0, 128.0]
+    assert mg.optimizer_completed_steps(oa) == 6 and mg.optimizer_completed_steps(ob) == 5
