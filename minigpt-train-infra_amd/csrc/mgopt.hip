@@ -46,6 +46,15 @@ constexpr bool kNtNormLoad = true;   // nontemporal gradient loads in pass 1
 // chunks (fewer partials for finalize), but caps of 1024-4096 measured
 // 0.1-0.15 ms slower per step on the Qwen3-8B set than one group per chunk
 constexpr uint32_t kNormGrid = 0xFFFFFFFFu;
+// The command processor hands work-groups to the 8 XCDs round-robin in
+// blockIdx order.  With the remap each XCD instead walks one contiguous range
+// of chunks, so its L2 and address-translation caches see 1/8 of the address
+// window instead of every eighth chunk of all of it.  Measured on the
+// Qwen3-8B-shaped set: pass 2 0.1-0.2 ms faster (within run-to-run spread),
+// pass 1 0.0-0.3 ms slower, so only pass 2 uses it.
+constexpr bool kXcdMapAdam = true;
+constexpr bool kXcdMapNorm = false;
+constexpr uint32_t kXcds = 8;
 
 struct DevTensor {
     float* param;   // fp32 param or fp32 master
@@ -165,6 +174,17 @@ __device__ __forceinline__ void store4(T* p, const Vec4<T>& r) {
 }
 
 __device__ __forceinline__ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// Work item of work-group `bid` in a grid of `n`: a bijection of [0, n).
+// Work-group bid runs on XCD bid % 8; XCD x gets items
+// [x*per + min(x, rem), ...) of length per + (x < rem), in order.
+template <bool kRemap>
+__device__ __forceinline__ uint32_t xcd_item(uint32_t bid, uint32_t n) {
+    if constexpr (!kRemap) return bid;
+    const uint32_t per = n / kXcds, rem = n % kXcds;
+    const uint32_t x = bid % kXcds;
+    return x * per + min(x, rem) + bid / kXcds;
+}
 
 // Native vector types for 16-byte (4 x fp32) and 8-byte (4 x 16-bit) accesses;
 // the nontemporal forms mark streamed data that no later access reuses.
@@ -295,11 +315,13 @@ __device__ __forceinline__ void norm_accum(float x, float inv, bool unscale, dou
 
 template <typename GT>
 __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
-    // grid-stride over the class's chunks in a fixed order: one partial per
-    // work-group, so the finalize kernel reads a few thousand partials
+    // grid-stride over the class's chunks in a fixed order: work-group slot r
+    // (XCD-remapped) sums chunks r, r + grid, ... into partial r, so the
+    // partials' order does not depend on the remapping
     double acc = 0.0;
     uint32_t bad = 0;
-    for (uint32_t cb = blockIdx.x; cb < a.count; cb += gridDim.x) {
+    const uint32_t slot = xcd_item<kXcdMapNorm>(blockIdx.x, gridDim.x);
+    for (uint32_t cb = slot; cb < a.count; cb += gridDim.x) {
     const Chunk ck = a.chunks[a.chunk_begin + cb];
     const GT* __restrict__ g = static_cast<const GT*>(a.grads[ck.tensor]);
     if (g != nullptr) {
@@ -339,7 +361,7 @@ __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
         p.sumsq = acc;
         p.nonfinite = bad;
         p.pad = 0;
-        a.partials[a.partial_base + blockIdx.x] = p;
+        a.partials[a.partial_base + slot] = p;
     }
 }
 
@@ -548,7 +570,7 @@ struct Group {
 
 template <typename GT, int LOWP>
 __global__ void __launch_bounds__(kBlock) adamw_kernel(const AdamArgs a) {
-    const uint32_t cidx = a.chunk_begin + blockIdx.x;
+    const uint32_t cidx = a.chunk_begin + xcd_item<kXcdMapAdam>(blockIdx.x, gridDim.x);
     const Chunk ck = a.chunks[cidx];
     GT* __restrict__ g = static_cast<GT*>(a.grads[ck.tensor]);
     if (g == nullptr) return;
