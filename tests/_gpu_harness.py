@@ -160,9 +160,10 @@ class Pair:
         self.outs.append(out)
         return out
 
-    def run(self, steps: int | None = None, oracle: bool = True) -> None:
+    def run(self, steps: int | None = None, oracle: bool = True, start: int = 1) -> None:
+        """Iterations start .. steps (default: the case's step count)."""
         c = self.case
-        for s in range(1, (steps or c.steps) + 1):
+        for s in range(start, (steps or c.steps) + 1):
             lr = mg.cosine_lr(s - 1, *c.lr_sched)
             mg.set_optimizer_lr(self.opt, lr)
             self.fill_grads(s)

@@ -12,7 +12,7 @@ import torch
 
 from oracle import oracle as O
 from tests._compare import RTOL_NORM, RTOL_STATE, exact_fraction, maxrel, rel
-from tests._gpu_harness import Case, Pair, host_grad, log, mg, syn, to_f32
+from tests._gpu_harness import Case, Pair, check_pair, host_grad, log, mg, syn, to_f32
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -255,6 +255,33 @@ def test_torch_adamw_state_dict_loads_and_continues():
     back = torch.optim.AdamW([torch.nn.Parameter(q.detach().cpu()) for q in gpu], lr=1e-3)
     back.load_state_dict({"state": {k: {n: t.cpu() for n, t in v.items()} for k, v in opt.state_dict()["state"].items()},
                           "param_groups": opt.state_dict()["param_groups"]})
+
+
+def test_state_assigned_in_param_dtype_is_picked_up():
+    """The reference's checkpoint-migration branch (src/minigpt/optim.py:242-251,
+    124-133) clears optimizer.state and assigns every parameter a dict whose
+    tensors were cast to the parameter's dtype (the step to fp32).  With bf16
+    parameters the moments and the master arrive as bf16; the optimizer keeps
+    them in its fp32 arenas from then on and continues exactly as the oracle
+    does from the same rounded state."""
+    shapes = [("w", (96, 40)), ("c", (4097,)), ("b", (40,))]
+    pair = Pair(Case(shapes=shapes, param_dtype="bf16", grad_dtype="bf16", steps=8, sigma=1e-3, tail=(1000, 100.0)))
+    pair.run(4)
+    saved = [{k: v.detach().cpu().clone() for k, v in pair.opt.state[p].items()} for p in pair.params]
+    assert all(set(st) == {"step", "exp_avg", "exp_avg_sq", "master_param"} for st in saved)
+    pair.opt.state.clear()
+    for p, st in zip(pair.params, saved):
+        pair.opt.state[p] = {k: v.to(device=p.device, dtype=torch.float32 if k == "step" else p.dtype)
+                             for k, v in st.items()}
+    for arrs in (pair.orc.m, pair.orc.v, pair.orc.p):
+        for i, a in enumerate(arrs):
+            arrs[i] = O.from_bf16(O.to_bf16(np.ascontiguousarray(a.ravel()))).reshape(a.shape)
+    pair.run(8, start=5)
+    for p in pair.params:
+        st = pair.opt.state[p]
+        assert st["exp_avg"].dtype == st["master_param"].dtype == torch.float32
+        assert float(st["step"]) == 8.0
+    check_pair(pair, label="migrated_state")
 
 
 def test_stock_torch_grad_scaler_drives_this_adamw():
