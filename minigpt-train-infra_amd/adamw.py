@@ -44,27 +44,34 @@ class _TrackedState(defaultdict):
 
     def __init__(self, owner: "AdamW"):
         super().__init__(dict)
-        self._owner = owner
+        # a weak reference: the optimizer owns this dict, and a cycle would keep
+        # its device arenas alive until the cyclic collector runs
+        self._owner = weakref.ref(owner)
+
+    def _dirty(self) -> None:
+        owner = self._owner()
+        if owner is not None:
+            owner._state_dirty = True
 
     def __setitem__(self, key, value):
         super().__setitem__(key, value)
-        self._owner._state_dirty = True
+        self._dirty()
 
     def __delitem__(self, key):
         super().__delitem__(key)
-        self._owner._state_dirty = True
+        self._dirty()
 
     def clear(self):
         super().clear()
-        self._owner._state_dirty = True
+        self._dirty()
 
     def update(self, *args, **kwargs):
         super().update(*args, **kwargs)
-        self._owner._state_dirty = True
+        self._dirty()
 
     def pop(self, *args):
         r = super().pop(*args)
-        self._owner._state_dirty = True
+        self._dirty()
         return r
 
     def __reduce__(self):

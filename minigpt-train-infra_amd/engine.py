@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import weakref
 from typing import Any, Sequence
 
 import numpy as np
@@ -52,7 +53,9 @@ def bias_correction_table(beta1: float, beta2: float, cap: int) -> list[float]:
 
 class _Engine:
     def __init__(self, optimizer: torch.optim.Optimizer, master_weights: bool | None, chunk_elems: int | None):
-        self.opt = optimizer
+        # weak: the optimizer owns the engine, and a reference cycle would hold
+        # the arenas (up to 100+ GB) until the cyclic collector happens to run
+        self._opt_ref = weakref.ref(optimizer)
         self.params: list[torch.Tensor] = []
         self.group_index: list[int] = []
         seen: set[int] = set()
@@ -139,6 +142,13 @@ class _Engine:
         self.bc_keys: list[tuple[float, float]] = []
         self.bc_table: torch.Tensor | None = None
         self.reset_iteration()
+
+    @property
+    def opt(self) -> torch.optim.Optimizer:
+        opt = self._opt_ref()
+        if opt is None:
+            raise RuntimeError("the optimizer that owned this engine was released")
+        return opt
 
     # ------------------------------------------------------------------ plan
     def close(self) -> None:

@@ -284,6 +284,32 @@ def test_state_assigned_in_param_dtype_is_picked_up():
     check_pair(pair, label="migrated_state")
 
 
+def test_dropping_the_optimizer_frees_its_arenas_at_once():
+    """The engine's arenas are released when the optimizer is dropped, without
+    waiting for Python's cycle collector."""
+    import gc
+
+    params = _params([(1024, 1024), (1024,)], torch.bfloat16)
+    opt = mg.AdamW(params, lr=1e-3)
+    sc = mg.GradScaler("cuda", init_scale=1024.0)
+    sc.scale(torch.ones((), device=DEV))
+    _grads(params, 1, 1e-3 * 1024)
+    sc.unscale_(opt)
+    mg.clip_grad_norm_(params, 1.0)
+    sc.step(opt)
+    sc.update()
+    torch.cuda.synchronize()
+    held = torch.cuda.memory_allocated()
+    gc.disable()
+    try:
+        del opt
+        freed = held - torch.cuda.memory_allocated()
+    finally:
+        gc.enable()
+    # exp_avg + exp_avg_sq + master: 3 x 4 B per element
+    assert freed >= 3 * 4 * (1024 * 1024 + 1024), freed
+
+
 def test_stock_torch_grad_scaler_drives_this_adamw():
     """torch.amp.GradScaler hands found_inf / grad_scale to an optimizer with
     _step_supports_amp_scaling; the results equal this package's scaler."""

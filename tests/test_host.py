@@ -161,6 +161,25 @@ def test_adamw_argument_validation(mg):
     assert set(ref.param_groups[0]) == set(opt.param_groups[0])
 
 
+def test_optimizer_is_released_without_the_cycle_collector(mg):
+    """No reference cycle through optimizer.state: dropping the optimizer
+    frees it (and, on a GPU, its arenas) at once."""
+    import gc
+    import weakref
+
+    p = nn.Parameter(torch.zeros(4))
+    opt = mg.AdamW([p], lr=1e-3)
+    opt.state[p]["note"] = 1
+    assert opt._state_dirty
+    ref = weakref.ref(opt)
+    gc.disable()
+    try:
+        del opt
+        assert ref() is None
+    finally:
+        gc.enable()
+
+
 def test_scheduler_helpers(mg):
     model = TinyGPT()
     opt = mg.AdamW(mg.build_adamw_param_groups(model, 0.1), lr=1.0)
