@@ -120,7 +120,7 @@ def read_traffic(name: str) -> float | None:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=15)
     ap.add_argument("--workload", default="qwen3_8b", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -239,6 +239,10 @@ def main() -> int:
         "achieved_GBps": achieved_step,
         "pct_of_hbm_peak": 100.0 * achieved_step / HBM_PEAK_GBPS,
         "bytes_per_param": bpp,
+        # what the two passes move: the gradients are read once more by the norm pass
+        "implementation_bytes_per_param": bpp + grad_bytes,
+        "implementation_GBps": (bpp + grad_bytes) * n_params / step_s / 1e9,
+        "skipped_steps": skipped,
         "passes_ms": {"norm": norm_ms, "adamw": adamw_ms},
         "roofline": {
             "bound": "hbm",
