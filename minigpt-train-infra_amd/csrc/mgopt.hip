@@ -372,6 +372,9 @@ __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
 __global__ void __launch_bounds__(kFinalizeBlock)
     finalize_kernel(const Partial* partials, int64_t n, double max_norm, float* norm_out, float* coef_out,
                     float* found_inf_out, Window* win) {
+    // each thread sums partials tid, tid + 1024, ... in that order (45 us for
+    // the 125K partials of the Qwen3-8B set: one CU's memory parallelism;
+    // unrolling the loads 8-deep measured the same)
     double s = 0.0;
     uint32_t f = 0;
     for (int64_t i = threadIdx.x; i < n; i += kFinalizeBlock) {
