@@ -110,12 +110,18 @@ def load_library() -> ctypes.CDLL:
         return _lib
 
 
+_gpu_seen = False
+
+
 def lib() -> ctypes.CDLL:
     """The library, for calls that launch GPU work: requires a visible GPU."""
-    import torch
+    global _gpu_seen
+    if not _gpu_seen:
+        import torch
 
-    if not torch.cuda.is_available():
-        raise RuntimeError("libmgopt needs a ROCm GPU; none is visible (there is no CPU fallback)")
+        if not torch.cuda.is_available():
+            raise RuntimeError("libmgopt needs a ROCm GPU; none is visible (there is no CPU fallback)")
+        _gpu_seen = True
     return load_library()
 
 
@@ -147,9 +153,18 @@ def check(rc: int, what: str) -> None:
 
 
 def stream_handle(device) -> int:
+    """The raw HIP stream behind torch's current stream on `device` (what
+    torch.cuda.current_stream(device).cuda_stream returns, without building a
+    Stream object: this is called several times per optimizer step)."""
     import torch
 
-    return torch.cuda.current_stream(device).cuda_stream
+    index = device.index if isinstance(device, torch.device) else device
+    if index is None:
+        index = torch.cuda.current_device()
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return raw(index)
+    return torch.cuda.current_stream(index).cuda_stream
 
 
 def dtype_code(dtype) -> int:

@@ -141,6 +141,8 @@ class _Engine:
         self.bc_cap = 0
         self.bc_keys: list[tuple[float, float]] = []
         self.bc_table: torch.Tensor | None = None
+        self.hp = None                       # GroupHparams array passed to mgopt_adamw_step
+        self.hp_key: list[tuple] | None = None
         self.reset_iteration()
 
     @property
@@ -261,7 +263,7 @@ class _Engine:
         if self.plan is None or dtypes_t != self.plan_grad_dtypes:
             self._build_plan(dtypes_t)
         arr = ctypes.cast(ctypes.c_char_p(gptrs), ctypes.POINTER(ctypes.c_void_p))
-        N.check(N.lib().mgopt_plan_set_grads(ctypes.c_void_p(self.plan), arr, ctypes.c_void_p(N.stream_handle(self.device))),
+        N.check(N.lib().mgopt_plan_set_grads(self.plan, arr, self._stream()),
                 "mgopt_plan_set_grads")
         self.grad_ptr_bytes, self.grad_dtype_bytes = gptrs, gdt
         if self.grad_source is not None:
@@ -289,8 +291,8 @@ class _Engine:
         self.norm_done = False
         return self.found_inf
 
-    def _stream(self) -> ctypes.c_void_p:
-        return ctypes.c_void_p(N.stream_handle(self.device))
+    def _stream(self) -> int:
+        return N.stream_handle(self.device)
 
     def norm(self, max_norm: float | None) -> torch.Tensor:
         """Pass 1 + finalize; returns the pre-clip total norm (fresh 0-dim tensor)."""
@@ -305,16 +307,15 @@ class _Engine:
 
     def _launch_norm(self, norm_out: torch.Tensor | None, max_norm: float | None) -> None:
         """max_norm None: no clipping requested, the coefficient is not written."""
-        lib = N.lib()
         scale = self.scale_src
         N.check(
-            lib.mgopt_grad_norm(
-                ctypes.c_void_p(self.plan),
-                ctypes.c_void_p(scale.data_ptr() if scale is not None else None),
-                ctypes.c_double(float(max_norm) if max_norm is not None else 0.0),
-                ctypes.c_void_p(norm_out.data_ptr() if norm_out is not None else None),
-                ctypes.c_void_p(self.coef.data_ptr() if max_norm is not None else None),
-                ctypes.c_void_p(self.found_inf.data_ptr() if scale is not None else None),
+            N.lib().mgopt_grad_norm(
+                self.plan,
+                scale.data_ptr() if scale is not None else None,
+                float(max_norm) if max_norm is not None else 0.0,
+                norm_out.data_ptr() if norm_out is not None else None,
+                self.coef.data_ptr() if max_norm is not None else None,
+                self.found_inf.data_ptr() if scale is not None else None,
                 self._stream(),
             ),
             "mgopt_grad_norm",
@@ -340,7 +341,7 @@ class _Engine:
             return
         if self.plan is None:
             self.prepare()
-        N.check(N.lib().mgopt_sync_master(ctypes.c_void_p(self.plan), self._stream()), "mgopt_sync_master")
+        N.check(N.lib().mgopt_sync_master(self.plan, self._stream()), "mgopt_sync_master")
         self.master_synced = True
 
     def step(self, found_inf: torch.Tensor | None = None, grad_scale: torch.Tensor | None = None,
@@ -359,26 +360,28 @@ class _Engine:
             if grad_scale is not None:
                 scale = grad_scale
             skip_src = found_inf
-        hp = (N.GroupHparams * len(groups))()
-        for gi, g in enumerate(groups):
+        key = []
+        for g in groups:
             if g.get("amsgrad", False):
                 raise NotImplementedError("amsgrad is not supported by mgopt AdamW")
             lr = g["lr"]
-            hp[gi].lr = float(lr.item() if isinstance(lr, torch.Tensor) else lr)
-            hp[gi].weight_decay = float(g["weight_decay"])
-            hp[gi].beta1 = float(g["betas"][0])
-            hp[gi].beta2 = float(g["betas"][1])
-            hp[gi].eps = float(g["eps"])
-            hp[gi].maximize = 1 if g.get("maximize", False) else 0
+            key.append((float(lr.item() if isinstance(lr, torch.Tensor) else lr), float(g["weight_decay"]),
+                        float(g["betas"][0]), float(g["betas"][1]), float(g["eps"]), bool(g.get("maximize", False))))
+        if key != self.hp_key:
+            # the hyperparameter block is rewritten only when a group changed
+            hp = (N.GroupHparams * len(groups))()
+            for d, (lr, wd, b1, b2, eps, maximize) in zip(hp, key):
+                d.lr, d.weight_decay, d.beta1, d.beta2, d.eps, d.maximize = lr, wd, b1, b2, eps, int(maximize)
+            self.hp, self.hp_key = hp, key
         self.t_bound += 1
         self._ensure_bc(groups)
         flags = N.WRITEBACK_GRADS if writeback else 0
         N.check(
             N.lib().mgopt_adamw_step(
-                ctypes.c_void_p(self.plan), hp, ctypes.c_void_p(self.bc_table.data_ptr()), self.bc_cap,
-                ctypes.c_void_p(scale.data_ptr() if scale is not None else None),
-                ctypes.c_void_p(self.coef.data_ptr() if self.clip_pending else None),
-                ctypes.c_void_p(skip_src.data_ptr() if skip_src is not None else None),
+                self.plan, self.hp, self.bc_table.data_ptr(), self.bc_cap,
+                scale.data_ptr() if scale is not None else None,
+                self.coef.data_ptr() if self.clip_pending else None,
+                skip_src.data_ptr() if skip_src is not None else None,
                 flags, self._stream(),
             ),
             "mgopt_adamw_step",

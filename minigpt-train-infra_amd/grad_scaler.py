@@ -169,12 +169,15 @@ class GradScaler:
                 raise AssertionError("No inf checks were recorded prior to update.")
             if len(found) > 8:
                 raise RuntimeError("at most 8 optimizers per scaler")
-            arr = (ctypes.c_void_p * len(found))(*[f.data_ptr() for f in found])
+            ptrs = tuple(f.data_ptr() for f in found)
+            if getattr(self, "_found_ptrs", None) != ptrs:
+                # the optimizers' found_inf tensors persist: the pointer array is rebuilt only when they change
+                self._found_ptrs, self._found_arr = ptrs, (ctypes.c_void_p * len(ptrs))(*ptrs)
             N.check(
                 N.lib().mgopt_scaler_update(
-                    ctypes.c_void_p(_scale.data_ptr()), ctypes.c_void_p(_tracker.data_ptr()), arr, len(found),
+                    _scale.data_ptr(), _tracker.data_ptr(), self._found_arr, len(ptrs),
                     float(self._growth_factor), float(self._backoff_factor), int(self._growth_interval),
-                    ctypes.c_void_p(N.stream_handle(_scale.device)),
+                    N.stream_handle(_scale.device),
                 ),
                 "mgopt_scaler_update",
             )
@@ -256,6 +259,8 @@ class GradScaler:
             state["_init_growth_tracker"] = self._get_growth_tracker()
             state["_scale"] = None
             state["_growth_tracker"] = None
+        state.pop("_found_ptrs", None)   # device addresses and a ctypes array: not part of the state
+        state.pop("_found_arr", None)
         return state
 
     def __setstate__(self, state: dict[str, Any]) -> None:
