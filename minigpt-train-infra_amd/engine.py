@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import sys
 import weakref
 from typing import Any, Sequence
 
@@ -159,8 +160,7 @@ class _Engine:
             self.plan = None
 
     def __del__(self):
-        import sys
-
+        # (no imports here: at interpreter shutdown the import system is gone)
         if sys.is_finalizing():
             return  # the HIP runtime may already be gone; the process releases everything
         try:
