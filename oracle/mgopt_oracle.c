@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product loads this library; only
  * tests/, __graft_entry__.smoke() and the cpu_baseline leg of bench.py do, and
- * only as the checker.
+ * only as the reference results that the GPU path is compared against.
  *
  * What it restates.  The reference's training loop runs, once per iteration
  * (train.py:483-491):

@@ -1,6 +1,7 @@
 """Python face of the CPU oracle (mgopt_oracle.c).  TEST INFRASTRUCTURE ONLY:
 imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg,
-as the checker; never by the product package.
+as the reference results the GPU path is compared against; never by the
+product package.
 
 OracleRun restates one iteration of the reference's training loop
 (train.py:483-491) over numpy float32 arrays: GradScaler.unscale_, then
