@@ -130,7 +130,7 @@ def main() -> int:
                          "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path (use --gpus 1)", file=sys.stderr)
+        print("bench.py measures one GPU only: the optimizer step here has no multi-GPU path (use --gpus 1)", file=sys.stderr)
         return 2
 
     dev = torch.device("cuda:0")

@@ -1,5 +1,5 @@
-"""Pins the CPU oracle (oracle/mgopt_oracle.c) before it is trusted as the
-checker of the GPU path.
+"""Pins the CPU oracle (oracle/mgopt_oracle.c) before the GPU path is compared
+against it.
 
 Three kinds of evidence, none of which retypes the oracle's formulas:
   1. golden vectors written by torch 2.10.0 on the CPU (tests/golden/), i.e.
