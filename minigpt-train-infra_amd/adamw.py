@@ -127,6 +127,8 @@ class AdamW(torch.optim.Optimizer):
             raise NotImplementedError("amsgrad is not supported by this AdamW")
         if differentiable:
             raise NotImplementedError("differentiable=True is not supported by this AdamW")
+        if capturable:
+            raise NotImplementedError("capturable=True (graph capture of the step) is not supported by this AdamW")
         defaults = dict(
             lr=lr,
             betas=betas,

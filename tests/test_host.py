@@ -154,6 +154,10 @@ def test_adamw_argument_validation(mg):
             mg.AdamW(p, **kw)
     with pytest.raises(NotImplementedError):
         mg.AdamW(p, amsgrad=True)
+    with pytest.raises(NotImplementedError):
+        mg.AdamW(p, capturable=True)
+    with pytest.raises(NotImplementedError):
+        mg.AdamW(p, differentiable=True)
     opt = mg.AdamW(p, lr=2e-3, betas=(0.8, 0.99), eps=1e-7, weight_decay=0.05)
     g = opt.param_groups[0]
     assert (g["lr"], g["betas"], g["eps"], g["weight_decay"], g["decoupled_weight_decay"]) == (2e-3, (0.8, 0.99), 1e-7, 0.05, True)
