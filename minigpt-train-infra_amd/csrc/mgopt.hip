@@ -322,38 +322,38 @@ __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
     uint32_t bad = 0;
     const uint32_t slot = xcd_item<kXcdMapNorm>(blockIdx.x, gridDim.x);
     for (uint32_t cb = slot; cb < a.count; cb += gridDim.x) {
-    const Chunk ck = a.chunks[a.chunk_begin + cb];
-    const GT* __restrict__ g = static_cast<const GT*>(a.grads[ck.tensor]);
-    if (g != nullptr) {
-        const int64_t numel = a.tensors[ck.tensor].numel;
-        const int64_t start = static_cast<int64_t>(ck.index) * a.chunk_elems;
-        const int64_t len = min(a.chunk_elems, numel - start);
-        g += start;
-        const bool unscale = a.scale != nullptr;
-        const float inv = unscale ? static_cast<float>(1.0 / static_cast<double>(*a.scale)) : 1.0f;
-        int64_t done = 0;
-        if (aligned(g, sizeof(GT) * kVec)) {
-            const int64_t nvec = len / kVec;
-            int64_t i = threadIdx.x;
-            for (; i + (kNormUnroll - 1) * kBlock < nvec; i += kNormUnroll * kBlock) {
-                float x[kNormUnroll][kVec];
+        const Chunk ck = a.chunks[a.chunk_begin + cb];
+        const GT* __restrict__ g = static_cast<const GT*>(a.grads[ck.tensor]);
+        if (g != nullptr) {
+            const int64_t numel = a.tensors[ck.tensor].numel;
+            const int64_t start = static_cast<int64_t>(ck.index) * a.chunk_elems;
+            const int64_t len = min(a.chunk_elems, numel - start);
+            g += start;
+            const bool unscale = a.scale != nullptr;
+            const float inv = unscale ? static_cast<float>(1.0 / static_cast<double>(*a.scale)) : 1.0f;
+            int64_t done = 0;
+            if (aligned(g, sizeof(GT) * kVec)) {
+                const int64_t nvec = len / kVec;
+                int64_t i = threadIdx.x;
+                for (; i + (kNormUnroll - 1) * kBlock < nvec; i += kNormUnroll * kBlock) {
+                    float x[kNormUnroll][kVec];
 #pragma unroll
-                for (int u = 0; u < kNormUnroll; ++u) load_grad<GT, kNtNormLoad, kVec>(g + (i + u * kBlock) * kVec, x[u]);
+                    for (int u = 0; u < kNormUnroll; ++u) load_grad<GT, kNtNormLoad, kVec>(g + (i + u * kBlock) * kVec, x[u]);
 #pragma unroll
-                for (int u = 0; u < kNormUnroll; ++u)
+                    for (int u = 0; u < kNormUnroll; ++u)
 #pragma unroll
-                    for (int k = 0; k < kVec; ++k) norm_accum(x[u][k], inv, unscale, acc, bad);
+                        for (int k = 0; k < kVec; ++k) norm_accum(x[u][k], inv, unscale, acc, bad);
+                }
+                for (; i < nvec; i += kBlock) {
+                    float x[kVec];
+                    load_grad<GT, kNtNormLoad, kVec>(g + i * kVec, x);
+#pragma unroll
+                    for (int k = 0; k < kVec; ++k) norm_accum(x[k], inv, unscale, acc, bad);
+                }
+                done = nvec * kVec;
             }
-            for (; i < nvec; i += kBlock) {
-                float x[kVec];
-                load_grad<GT, kNtNormLoad, kVec>(g + i * kVec, x);
-#pragma unroll
-                for (int k = 0; k < kVec; ++k) norm_accum(x[k], inv, unscale, acc, bad);
-            }
-            done = nvec * kVec;
+            for (int64_t i = done + threadIdx.x; i < len; i += kBlock) norm_accum(GradIO<GT>::to_f32(g[i]), inv, unscale, acc, bad);
         }
-        for (int64_t i = done + threadIdx.x; i < len; i += kBlock) norm_accum(GradIO<GT>::to_f32(g[i]), inv, unscale, acc, bad);
-    }
     }
     block_reduce<kBlock>(acc, bad);
     if (threadIdx.x == 0) {
