@@ -42,10 +42,12 @@ constexpr bool kNtLoad = true;       // nontemporal loads of grad/param/exp_avg/
 constexpr bool kNtStore = true;      // nontemporal stores of param/exp_avg/exp_avg_sq
 constexpr int kNormUnroll = 2;       // pass-1 4-element accesses in flight per thread
 constexpr bool kNtNormLoad = true;   // nontemporal gradient loads in pass 1
-// pass-1 work-groups per dtype class; a cap makes each one stride over several
-// chunks (fewer partials for finalize), but caps of 1024-4096 measured
-// 0.1-0.15 ms slower per step on the Qwen3-8B set than one group per chunk
-constexpr uint32_t kNormGrid = 0xFFFFFFFFu;
+// pass-1 work-groups cover about kNormSpan elements each: a contiguous run of
+// max(1, kNormSpan / chunk_elems) chunks, so smaller pass-2 chunks do not
+// multiply the partials the finalize kernel reads.  (A grid-stride form with
+// 1024-4096 work-groups per class measured 0.1-0.15 ms slower per step on the
+// Qwen3-8B set than 64K elements per work-group.)
+constexpr int64_t kNormSpan = 65536;
 // The command processor hands work-groups to the 8 XCDs round-robin in
 // blockIdx order.  With the remap each XCD instead walks one contiguous range
 // of chunks, so its L2 and address-translation caches see 1/8 of the address
@@ -264,6 +266,7 @@ struct NormArgs {
     uint32_t chunk_begin;
     uint32_t count;         // chunks of this launch's class
     uint32_t partial_base;  // first partial slot of this launch
+    uint32_t group;         // consecutive chunks per work-group
 };
 
 __device__ __forceinline__ double wave_sum(double x) {
@@ -315,19 +318,25 @@ __device__ __forceinline__ void norm_accum(float x, float inv, bool unscale, dou
 
 template <typename GT>
 __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
-    // grid-stride over the class's chunks in a fixed order: work-group slot r
-    // (XCD-remapped) sums chunks r, r + grid, ... into partial r, so the
-    // partials' order does not depend on the remapping
+    // work-group slot r (XCD-remapped) sums chunks [r * group, (r + 1) * group)
+    // of its class, in order, into partial r: the partials' order does not
+    // depend on the remapping.  Consecutive chunks of one tensor are one
+    // contiguous range of its gradient and are read as such.
     double acc = 0.0;
     uint32_t bad = 0;
     const uint32_t slot = xcd_item<kXcdMapNorm>(blockIdx.x, gridDim.x);
-    for (uint32_t cb = slot; cb < a.count; cb += gridDim.x) {
+    const uint64_t first = static_cast<uint64_t>(slot) * a.group;
+    const uint64_t last = min(static_cast<uint64_t>(a.count), first + a.group);
+    for (uint64_t cb = first; cb < last;) {
         const Chunk ck = a.chunks[a.chunk_begin + cb];
+        uint64_t run = 1;  // chunks of a tensor are stored in index order, one after another
+        while (cb + run < last && a.chunks[a.chunk_begin + cb + run].tensor == ck.tensor) ++run;
+        cb += run;
         const GT* __restrict__ g = static_cast<const GT*>(a.grads[ck.tensor]);
         if (g != nullptr) {
             const int64_t numel = a.tensors[ck.tensor].numel;
             const int64_t start = static_cast<int64_t>(ck.index) * a.chunk_elems;
-            const int64_t len = min(a.chunk_elems, numel - start);
+            const int64_t len = min(static_cast<int64_t>(run) * a.chunk_elems, numel - start);
             g += start;
             const bool unscale = a.scale != nullptr;
             const float inv = unscale ? static_cast<float>(1.0 / static_cast<double>(*a.scale)) : 1.0f;
@@ -786,7 +795,8 @@ struct mgopt_plan {
         int32_t lowp_dtype;
         uint32_t begin;
         uint32_t count;
-        uint32_t norm_grid;     // work-groups of the norm pass (<= count)
+        uint32_t norm_grid;     // work-groups of the norm pass: ceil(count / norm_group)
+        uint32_t norm_group;    // consecutive chunks per norm work-group
         uint32_t partial_base;  // first partial slot of the class
     };
     int64_t n_partials = 0;
@@ -810,7 +820,8 @@ int launch_check(const char* what) {
 
 template <typename GT>
 int launch_norm(const mgopt_plan* P, const mgopt_plan::Class& c, const float* scale, hipStream_t s) {
-    NormArgs a{P->d_tensors, P->d_chunks, P->d_grads, P->d_partials, scale, P->chunk_elems, c.begin, c.count, c.partial_base};
+    NormArgs a{P->d_tensors, P->d_chunks, P->d_grads, P->d_partials, scale, P->chunk_elems, c.begin, c.count, c.partial_base,
+               c.norm_group};
     hipLaunchKernelGGL(norm_kernel<GT>, dim3(c.norm_grid), dim3(kBlock), 0, s, a);
     return launch_check("norm_kernel");
 }
@@ -905,7 +916,8 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
             for (int64_t k = 0; k < nch; ++k) chunks.push_back(Chunk{static_cast<uint32_t>(i), static_cast<uint32_t>(k)});
         }
         c.count = static_cast<uint32_t>(chunks.size() - c.begin);
-        c.norm_grid = std::min<uint32_t>(c.count, kNormGrid);
+        c.norm_group = static_cast<uint32_t>(std::max<int64_t>(1, kNormSpan / chunk_elems));
+        c.norm_grid = (c.count + c.norm_group - 1) / c.norm_group;
         c.partial_base = static_cast<uint32_t>(P->n_partials);
         P->n_partials += c.norm_grid;
         if (c.count) P->classes.push_back(c);
