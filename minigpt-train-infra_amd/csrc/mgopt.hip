@@ -703,7 +703,19 @@ __global__ void __launch_bounds__(kBlock)
     const int64_t start = static_cast<int64_t>(ck.index) * chunk_elems;
     const int64_t len = min(chunk_elems, tensors[ck.tensor].numel - start);
     g += start;
-    for (int64_t i = threadIdx.x; i < len; i += kBlock) g[i] = GradIO<GT>::from_f32(GradIO<GT>::to_f32(g[i]) * coef);
+    int64_t done = 0;
+    if (aligned(g, sizeof(GT) * 4)) {
+        // four elements per thread per access, as torch's vectorised _foreach_mul_ reads them
+        const int64_t nvec = len / 4;
+        for (int64_t i = threadIdx.x; i < nvec; i += kBlock) {
+            Vec4<GT> q = load4(g + 4 * i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) q.e[k] = GradIO<GT>::from_f32(GradIO<GT>::to_f32(q.e[k]) * coef);
+            store4(g + 4 * i, q);
+        }
+        done = nvec * 4;
+    }
+    for (int64_t i = done + threadIdx.x; i < len; i += kBlock) g[i] = GradIO<GT>::from_f32(GradIO<GT>::to_f32(g[i]) * coef);
 }
 
 template <typename LT>
@@ -715,7 +727,17 @@ __global__ void __launch_bounds__(kBlock)
     const int64_t len = min(chunk_elems, T.numel - start);
     const LT* l = static_cast<const LT*>(T.lowp) + start;
     float* p = T.param + start;
-    for (int64_t i = threadIdx.x; i < len; i += kBlock) p[i] = GradIO<LT>::to_f32(l[i]);
+    int64_t done = 0;
+    if (aligned(l, sizeof(LT) * 4) && aligned(p, 16)) {
+        const int64_t nvec = len / 4;
+        for (int64_t i = threadIdx.x; i < nvec; i += kBlock) {
+            const Vec4<LT> q = load4(l + 4 * i);
+            store4(p + 4 * i, Vec4<float>{{GradIO<LT>::to_f32(q.e[0]), GradIO<LT>::to_f32(q.e[1]),
+                                           GradIO<LT>::to_f32(q.e[2]), GradIO<LT>::to_f32(q.e[3])}});
+        }
+        done = nvec * 4;
+    }
+    for (int64_t i = done + threadIdx.x; i < len; i += kBlock) p[i] = GradIO<LT>::to_f32(l[i]);
 }
 
 __device__ __host__ __forceinline__ uint64_t mix64(uint64_t x) {
