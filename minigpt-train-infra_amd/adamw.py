@@ -248,6 +248,10 @@ class AdamW(torch.optim.Optimizer):
             for p, g in zip(self._get_engine().params, self._grad_views):
                 if p.grad is not g:
                     p.grad = g
+        elif set_to_none and self._engine is not None and self._engine.grad_source is None:
+            # the per-parameter `p.grad = None` loop of Optimizer.zero_grad, done natively
+            # (3.4 ms of Python at 20,000 parameters)
+            self._engine.clear_grads()
         else:
             super().zero_grad(set_to_none=set_to_none)
         if self._engine is not None:

@@ -82,6 +82,15 @@ class ParamSet {
         return py::bytes(pp);
     }
 
+    // zero_grad(set_to_none=True) over every parameter: drops each .grad, as
+    // the per-parameter `p.grad = None` of torch.optim.Optimizer.zero_grad
+    // does, without a Python-level loop.
+    void clear_grads() {
+        for (at::Tensor& p : params_) {
+            if (p.grad().defined()) p.mutable_grad().reset();
+        }
+    }
+
     size_t size() const { return params_.size(); }
 
   private:
@@ -96,5 +105,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         .def(py::init<std::vector<at::Tensor>, std::vector<c10::optional<at::Tensor>>>())
         .def("gather", &ParamSet::gather)
         .def("param_ptrs", &ParamSet::param_ptrs)
+        .def("clear_grads", &ParamSet::clear_grads)
         .def("__len__", &ParamSet::size);
 }

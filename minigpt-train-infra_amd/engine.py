@@ -228,6 +228,10 @@ class _Engine:
         self._prepare()
         self.prepared = True
 
+    def clear_grads(self) -> None:
+        """zero_grad(set_to_none=True) in one native pass over the parameters."""
+        self._param_set().clear_grads()
+
     def _param_set(self):
         if self.pset is None:
             self.pset = N.host().ParamSet(self.params, [] if self.grad_source is None else self.grad_source)

@@ -184,6 +184,26 @@ def test_optimizer_is_released_without_the_cycle_collector(mg):
         gc.enable()
 
 
+def test_native_clear_grads_drops_every_grad():
+    """zero_grad(set_to_none=True)'s native form: every .grad becomes None,
+    and the pointer gather then reports no gradient for any parameter."""
+    import numpy as np
+
+    native = importlib.import_module("minigpt-train-infra_amd._native")
+    params = [nn.Parameter(torch.zeros(n)) for n in (3, 1, 4096)]
+    for p in params:
+        p.grad = torch.ones_like(p)
+    ps = native.host().ParamSet(params, [])
+    _, gptrs, gdt, _ = ps.gather()
+    assert np.all(np.frombuffer(gptrs, np.int64) != 0) and np.all(np.frombuffer(gdt, np.int8) == 0)
+    ps.clear_grads()
+    assert all(p.grad is None for p in params)
+    _, gptrs, gdt, _ = ps.gather()
+    assert np.all(np.frombuffer(gptrs, np.int64) == 0) and np.all(np.frombuffer(gdt, np.int8) == -1)
+    params[1].grad = torch.full((1,), 2.0)          # autograd can attach new grads afterwards
+    assert float(params[1].grad) == 2.0
+
+
 def test_scheduler_helpers(mg):
     model = TinyGPT()
     opt = mg.AdamW(mg.build_adamw_param_groups(model, 0.1), lr=1.0)
