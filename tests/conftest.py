@@ -13,6 +13,15 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X); run with -m gpu")
 
 
+def pytest_sessionstart(session):
+    """Builds the libraries once when the tree has none (a fresh checkout);
+    a built tree is used as it is."""
+    built = [ROOT / "minigpt-train-infra_amd" / "_build" / "libmgopt.so",
+             ROOT / "minigpt-train-infra_amd" / "_build" / "host" / "mgopt_host.so"]
+    if not all(p.exists() for p in built):
+        importlib.import_module("__graft_entry__").build()
+
+
 @pytest.fixture(scope="session")
 def mg():
     """The package (its directory name has hyphens, so import it by name)."""
