@@ -28,6 +28,7 @@ import torch
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
+importlib.import_module("__graft_entry__").ensure_built()   # builds only on a fresh checkout
 mg = importlib.import_module("minigpt-train-infra_amd")
 syn = importlib.import_module("minigpt-train-infra_amd.synthetic")
 

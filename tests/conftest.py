@@ -16,10 +16,7 @@ def pytest_configure(config):
 def pytest_sessionstart(session):
     """Builds the libraries once when the tree has none (a fresh checkout);
     a built tree is used as it is."""
-    built = [ROOT / "minigpt-train-infra_amd" / "_build" / "libmgopt.so",
-             ROOT / "minigpt-train-infra_amd" / "_build" / "host" / "mgopt_host.so"]
-    if not all(p.exists() for p in built):
-        importlib.import_module("__graft_entry__").build()
+    importlib.import_module("__graft_entry__").ensure_built()
 
 
 @pytest.fixture(scope="session")
