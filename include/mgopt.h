@@ -92,7 +92,7 @@ typedef struct mgopt_plan mgopt_plan;
  * and in _foreach_norm's tensor lists, clip_grad.py:85-96).  steps_dev is a
  * caller-owned float[n_tensors] holding each tensor's AdamW step count
  * (torch/optim/adam.py:168-176 state["step"]).  chunk_elems must be a positive
- * multiple of 4096. */
+ * multiple of 512. */
 MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensors, int32_t n_groups,
                                 float* steps_dev, int64_t chunk_elems, mgopt_plan** out);
 

@@ -86,7 +86,7 @@ class AdamW(torch.optim.Optimizer):
     writeback_grads: also store the unscaled, clipped gradient into each
         .grad during the step (the reference leaves them in .grad;
         train.py never reads them after the step, so this is off by default).
-    chunk_elems: elements per pass-2 work-group (a multiple of 4096; default 16384).
+    chunk_elems: elements per pass-2 work-group (a multiple of 512).
     """
 
     # GradScaler.step hands found_inf/grad_scale to the optimizer instead of

@@ -31,7 +31,16 @@
 
 namespace {
 
-constexpr int kBlock = 512;          // work-group size of the streaming passes
+constexpr int kBlock = 512;          // work-group size of pass 1 and the helper kernels
+// Pass 2 runs one short work-group per chunk.  With the default 1024-element
+// chunks a 512-thread work-group gives one 4-element group to lanes 0-255
+// and lanes 256-511 retire at once: half of a CU's wave slots carry memory
+// traffic and work-groups turn over quickly.  Measured on MI355X against
+// 256-thread groups, 2048/4096/16384/65536-element chunks and LDS-reserved
+// caps of 2-5 work-groups per CU, this was the fastest or tied on the
+// 8.2B set and within 2 % of the best on 124M-2.5B sets.
+constexpr int kAdamBlock = 512;      // work-group size of pass 2
+constexpr size_t kAdamLds = 0;       // LDS bytes reserved per pass-2 work-group (0: no cap on work-groups per CU)
 constexpr int kFinalizeBlock = 1024; // single work-group of the finalize kernel
 constexpr int kVec = 4;              // elements per thread per access: 4 = one 16-B fp32 access per lane;
                                      // 8 (two adjacent 16-B accesses) measured 1.8x slower (32-B lane stride)
@@ -42,12 +51,12 @@ constexpr bool kNtLoad = true;       // nontemporal loads of grad/param/exp_avg/
 constexpr bool kNtStore = true;      // nontemporal stores of param/exp_avg/exp_avg_sq
 constexpr int kNormUnroll = 2;       // pass-1 4-element accesses in flight per thread
 constexpr bool kNtNormLoad = true;   // nontemporal gradient loads in pass 1
-// pass-1 work-groups cover about kNormSpan elements each: a contiguous run of
-// max(1, kNormSpan / chunk_elems) chunks, so smaller pass-2 chunks do not
-// multiply the partials the finalize kernel reads.  (A grid-stride form with
-// 1024-4096 work-groups per class measured 0.1-0.15 ms slower per step on the
-// Qwen3-8B set than 64K elements per work-group.)
-constexpr int64_t kNormSpan = 65536;
+// pass 1 has its own chunk table of kNormChunk elements per chunk and
+// work-group, whatever the pass-2 chunk size: the finalize kernel then reads
+// one partial per 64K elements.  (A grid-stride form with 1024-4096
+// work-groups per class measured 0.1-0.15 ms slower per step on the Qwen3-8B
+// set than 64K elements per work-group.)
+constexpr int64_t kNormChunk = 65536;
 // The command processor hands work-groups to the 8 XCDs round-robin in
 // blockIdx order.  With the remap each XCD instead walks one contiguous range
 // of chunks, so its L2 and address-translation caches see 1/8 of the address
@@ -266,7 +275,6 @@ struct NormArgs {
     uint32_t chunk_begin;
     uint32_t count;         // chunks of this launch's class
     uint32_t partial_base;  // first partial slot of this launch
-    uint32_t group;         // consecutive chunks per work-group
 };
 
 __device__ __forceinline__ double wave_sum(double x) {
@@ -318,51 +326,42 @@ __device__ __forceinline__ void norm_accum(float x, float inv, bool unscale, dou
 
 template <typename GT>
 __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
-    // work-group slot r (XCD-remapped) sums chunks [r * group, (r + 1) * group)
-    // of its class, in order, into partial r: the partials' order does not
-    // depend on the remapping.  Consecutive chunks of one tensor are one
-    // contiguous range of its gradient and are read as such.
+    // work-group slot r (XCD-remapped) sums pass-1 chunk r of its class into
+    // partial r: the partials' order does not depend on the remapping
     double acc = 0.0;
     uint32_t bad = 0;
     const uint32_t slot = xcd_item<kXcdMapNorm>(blockIdx.x, gridDim.x);
-    const uint64_t first = static_cast<uint64_t>(slot) * a.group;
-    const uint64_t last = min(static_cast<uint64_t>(a.count), first + a.group);
-    for (uint64_t cb = first; cb < last;) {
-        const Chunk ck = a.chunks[a.chunk_begin + cb];
-        uint64_t run = 1;  // chunks of a tensor are stored in index order, one after another
-        while (cb + run < last && a.chunks[a.chunk_begin + cb + run].tensor == ck.tensor) ++run;
-        cb += run;
-        const GT* __restrict__ g = static_cast<const GT*>(a.grads[ck.tensor]);
-        if (g != nullptr) {
-            const int64_t numel = a.tensors[ck.tensor].numel;
-            const int64_t start = static_cast<int64_t>(ck.index) * a.chunk_elems;
-            const int64_t len = min(static_cast<int64_t>(run) * a.chunk_elems, numel - start);
-            g += start;
-            const bool unscale = a.scale != nullptr;
-            const float inv = unscale ? static_cast<float>(1.0 / static_cast<double>(*a.scale)) : 1.0f;
-            int64_t done = 0;
-            if (aligned(g, sizeof(GT) * kVec)) {
-                const int64_t nvec = len / kVec;
-                int64_t i = threadIdx.x;
-                for (; i + (kNormUnroll - 1) * kBlock < nvec; i += kNormUnroll * kBlock) {
-                    float x[kNormUnroll][kVec];
+    const Chunk ck = a.chunks[a.chunk_begin + slot];
+    const GT* __restrict__ g = static_cast<const GT*>(a.grads[ck.tensor]);
+    if (g != nullptr) {
+        const int64_t numel = a.tensors[ck.tensor].numel;
+        const int64_t start = static_cast<int64_t>(ck.index) * a.chunk_elems;
+        const int64_t len = min(a.chunk_elems, numel - start);
+        g += start;
+        const bool unscale = a.scale != nullptr;
+        const float inv = unscale ? static_cast<float>(1.0 / static_cast<double>(*a.scale)) : 1.0f;
+        int64_t done = 0;
+        if (aligned(g, sizeof(GT) * kVec)) {
+            const int64_t nvec = len / kVec;
+            int64_t i = threadIdx.x;
+            for (; i + (kNormUnroll - 1) * kBlock < nvec; i += kNormUnroll * kBlock) {
+                float x[kNormUnroll][kVec];
 #pragma unroll
-                    for (int u = 0; u < kNormUnroll; ++u) load_grad<GT, kNtNormLoad, kVec>(g + (i + u * kBlock) * kVec, x[u]);
+                for (int u = 0; u < kNormUnroll; ++u) load_grad<GT, kNtNormLoad, kVec>(g + (i + u * kBlock) * kVec, x[u]);
 #pragma unroll
-                    for (int u = 0; u < kNormUnroll; ++u)
+                for (int u = 0; u < kNormUnroll; ++u)
 #pragma unroll
-                        for (int k = 0; k < kVec; ++k) norm_accum(x[u][k], inv, unscale, acc, bad);
-                }
-                for (; i < nvec; i += kBlock) {
-                    float x[kVec];
-                    load_grad<GT, kNtNormLoad, kVec>(g + i * kVec, x);
-#pragma unroll
-                    for (int k = 0; k < kVec; ++k) norm_accum(x[k], inv, unscale, acc, bad);
-                }
-                done = nvec * kVec;
+                    for (int k = 0; k < kVec; ++k) norm_accum(x[u][k], inv, unscale, acc, bad);
             }
-            for (int64_t i = done + threadIdx.x; i < len; i += kBlock) norm_accum(GradIO<GT>::to_f32(g[i]), inv, unscale, acc, bad);
+            for (; i < nvec; i += kBlock) {
+                float x[kVec];
+                load_grad<GT, kNtNormLoad, kVec>(g + i * kVec, x);
+#pragma unroll
+                for (int k = 0; k < kVec; ++k) norm_accum(x[k], inv, unscale, acc, bad);
+            }
+            done = nvec * kVec;
         }
+        for (int64_t i = done + threadIdx.x; i < len; i += kBlock) norm_accum(GradIO<GT>::to_f32(g[i]), inv, unscale, acc, bad);
     }
     block_reduce<kBlock>(acc, bad);
     if (threadIdx.x == 0) {
@@ -581,7 +580,7 @@ struct Group {
 };
 
 template <typename GT, int LOWP>
-__global__ void __launch_bounds__(kBlock) adamw_kernel(const AdamArgs a) {
+__global__ void __launch_bounds__(kAdamBlock) adamw_kernel(const AdamArgs a) {
     const uint32_t cidx = a.chunk_begin + xcd_item<kXcdMapAdam>(blockIdx.x, gridDim.x);
     const Chunk ck = a.chunks[cidx];
     GT* __restrict__ g = static_cast<GT*>(a.grads[ck.tensor]);
@@ -631,21 +630,21 @@ __global__ void __launch_bounds__(kBlock) adamw_kernel(const AdamArgs a) {
         // the first one is consumed, to keep more bytes in flight per wave
         const int64_t nvec = len / kVec;
         int64_t i = threadIdx.x;
-        for (; i + (kUnroll - 1) * kBlock < nvec; i += kUnroll * kBlock) {
+        for (; i + (kUnroll - 1) * kAdamBlock < nvec; i += kUnroll * kAdamBlock) {
             Group<GT> q[kUnroll];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) q[u].load(g, P, M, V, (i + u * kBlock) * kVec);
+            for (int u = 0; u < kUnroll; ++u) q[u].load(g, P, M, V, (i + u * kAdamBlock) * kVec);
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) q[u].template finish<LOWP>(g, P, M, V, L, (i + u * kBlock) * kVec, c, wb);
+            for (int u = 0; u < kUnroll; ++u) q[u].template finish<LOWP>(g, P, M, V, L, (i + u * kAdamBlock) * kVec, c, wb);
         }
-        for (; i < nvec; i += kBlock) {
+        for (; i < nvec; i += kAdamBlock) {
             Group<GT> q;
             q.load(g, P, M, V, i * kVec);
             q.template finish<LOWP>(g, P, M, V, L, i * kVec, c, wb);
         }
         done = nvec * kVec;
     }
-    for (int64_t i = done + threadIdx.x; i < len; i += kBlock) {
+    for (int64_t i = done + threadIdx.x; i < len; i += kAdamBlock) {
         float p = P[i], m = M[i], v = V[i];
         const float gc = adam_elem(GradIO<GT>::to_f32(g[i]), p, m, v, c);
         P[i] = p;
@@ -806,7 +805,8 @@ struct mgopt_plan {
     int64_t chunk_elems = 0;
     int64_t n_chunks = 0;
     DevTensor* d_tensors = nullptr;
-    Chunk* d_chunks = nullptr;
+    Chunk* d_chunks = nullptr;       // pass 2 (and helpers): chunk_elems elements per chunk
+    Chunk* d_norm_chunks = nullptr;  // pass 1: kNormChunk elements per chunk
     void** d_grads = nullptr;
     Partial* d_partials = nullptr;
     int* d_err = nullptr;
@@ -817,8 +817,8 @@ struct mgopt_plan {
         int32_t lowp_dtype;
         uint32_t begin;
         uint32_t count;
-        uint32_t norm_grid;     // work-groups of the norm pass: ceil(count / norm_group)
-        uint32_t norm_group;    // consecutive chunks per norm work-group
+        uint32_t norm_begin;    // first entry of the class in the pass-1 chunk table
+        uint32_t norm_count;    // pass-1 chunks (= work-groups = partials) of the class
         uint32_t partial_base;  // first partial slot of the class
     };
     int64_t n_partials = 0;
@@ -842,15 +842,15 @@ int launch_check(const char* what) {
 
 template <typename GT>
 int launch_norm(const mgopt_plan* P, const mgopt_plan::Class& c, const float* scale, hipStream_t s) {
-    NormArgs a{P->d_tensors, P->d_chunks, P->d_grads, P->d_partials, scale, P->chunk_elems, c.begin, c.count, c.partial_base,
-               c.norm_group};
-    hipLaunchKernelGGL(norm_kernel<GT>, dim3(c.norm_grid), dim3(kBlock), 0, s, a);
+    NormArgs a{P->d_tensors, P->d_norm_chunks, P->d_grads, P->d_partials, scale, kNormChunk, c.norm_begin, c.norm_count,
+               c.partial_base};
+    hipLaunchKernelGGL(norm_kernel<GT>, dim3(c.norm_count), dim3(kBlock), 0, s, a);
     return launch_check("norm_kernel");
 }
 
 template <typename GT, int LOWP>
 int launch_adamw(const AdamArgs& a, uint32_t count, hipStream_t s) {
-    hipLaunchKernelGGL((adamw_kernel<GT, LOWP>), dim3(count), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((adamw_kernel<GT, LOWP>), dim3(count), dim3(kAdamBlock), kAdamLds, s, a);
     return launch_check("adamw_kernel");
 }
 
@@ -887,8 +887,8 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
     *out = nullptr;
     if (n_tensors <= 0 || !descs) return fail(MGOPT_E_INVALID, "empty tensor list");
     if (n_groups <= 0 || n_groups > MGOPT_MAX_GROUPS) return fail(MGOPT_E_LIMIT, "n_groups must be in 1..16");
-    if (chunk_elems <= 0 || chunk_elems % 4096 != 0 || chunk_elems > (int64_t(1) << 30))
-        return fail(MGOPT_E_INVALID, "chunk_elems must be a positive multiple of 4096, at most 2^30");
+    if (chunk_elems <= 0 || chunk_elems % 512 != 0 || chunk_elems > (int64_t(1) << 30))
+        return fail(MGOPT_E_INVALID, "chunk_elems must be a positive multiple of 512, at most 2^30");
 
     // Validate and bucket tensors by (grad dtype, lowp dtype): one kernel instance per bucket.
     std::vector<std::vector<int32_t>> buckets(9);
@@ -919,7 +919,7 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
     if (grads_only && with_state) return fail(MGOPT_E_INVALID, "a plan is either grads-only or has optimizer state for every tensor");
     if (with_state && !steps_dev) return fail(MGOPT_E_INVALID, "steps_dev is NULL");
 
-    std::vector<Chunk> chunks;
+    std::vector<Chunk> chunks, norm_chunks;
     mgopt_plan* P = new mgopt_plan();
     P->n_tensors = n_tensors;
     P->n_groups = n_groups;
@@ -938,10 +938,14 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
             for (int64_t k = 0; k < nch; ++k) chunks.push_back(Chunk{static_cast<uint32_t>(i), static_cast<uint32_t>(k)});
         }
         c.count = static_cast<uint32_t>(chunks.size() - c.begin);
-        c.norm_group = static_cast<uint32_t>(std::max<int64_t>(1, kNormSpan / chunk_elems));
-        c.norm_grid = (c.count + c.norm_group - 1) / c.norm_group;
+        c.norm_begin = static_cast<uint32_t>(norm_chunks.size());
+        for (int32_t i : buckets[b]) {
+            const int64_t nch = (descs[i].numel + kNormChunk - 1) / kNormChunk;
+            for (int64_t k = 0; k < nch; ++k) norm_chunks.push_back(Chunk{static_cast<uint32_t>(i), static_cast<uint32_t>(k)});
+        }
+        c.norm_count = static_cast<uint32_t>(norm_chunks.size() - c.norm_begin);
         c.partial_base = static_cast<uint32_t>(P->n_partials);
-        P->n_partials += c.norm_grid;
+        P->n_partials += c.norm_count;
         if (c.count) P->classes.push_back(c);
         if (chunks.size() > 0xFFFFFFF0ull) {
             delete P;
@@ -961,6 +965,11 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
     if ((e = hipMalloc(&P->d_err, sizeof(int))) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc err"));
     if (P->n_chunks > 0) {
         if ((e = hipMalloc(&P->d_chunks, sizeof(Chunk) * P->n_chunks)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc chunks"));
+        if ((e = hipMalloc(&P->d_norm_chunks, sizeof(Chunk) * norm_chunks.size())) != hipSuccess)
+            return cleanup(hip_fail(e, "hipMalloc norm chunks"));
+        if ((e = hipMemcpy(P->d_norm_chunks, norm_chunks.data(), sizeof(Chunk) * norm_chunks.size(), hipMemcpyHostToDevice)) !=
+            hipSuccess)
+            return cleanup(hip_fail(e, "upload norm chunks"));
         if ((e = hipMalloc(&P->d_partials, sizeof(Partial) * P->n_partials)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc partials"));
         if ((e = hipMemcpy(P->d_chunks, chunks.data(), sizeof(Chunk) * P->n_chunks, hipMemcpyHostToDevice)) != hipSuccess)
             return cleanup(hip_fail(e, "upload chunks"));
@@ -995,6 +1004,7 @@ MGOPT_API int mgopt_plan_destroy(mgopt_plan* P) {
     (void)hipDeviceSynchronize();
     (void)hipFree(P->d_tensors);
     (void)hipFree(P->d_chunks);
+    (void)hipFree(P->d_norm_chunks);
     (void)hipFree(P->d_grads);
     (void)hipFree(P->d_partials);
     (void)hipFree(P->d_err);

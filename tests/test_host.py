@@ -117,7 +117,7 @@ def test_c_abi_rejects_bad_arguments_before_touching_the_gpu():
     assert b"empty" in lib.mgopt_last_error()
     assert lib.mgopt_plan_create(descs, 1, 17, None, 65536, ctypes.byref(plan)) == 10003
     assert lib.mgopt_plan_create(descs, 1, 1, None, 1000, ctypes.byref(plan)) == 10001
-    assert b"multiple of 4096" in lib.mgopt_last_error()
+    assert b"multiple of 512" in lib.mgopt_last_error()
     descs[0].grad_dtype = 7
     assert lib.mgopt_plan_create(descs, 1, 1, None, 65536, ctypes.byref(plan)) == 10001
     descs[0].grad_dtype = native.F32
