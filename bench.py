@@ -10,6 +10,7 @@ Default workload: the Qwen3-8B-shaped parameter set (399 tensors,
 exp_avg_sq (131 GB resident), synthetic data.  Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+    python bench.py --vs-torch [--workload NAME]   # torch's own GPU step beside this one
 """
 
 from __future__ import annotations
@@ -53,8 +54,10 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def build_workload(name: str, dev: torch.device):
-    spec = WORKLOADS[name]
+def build_workload(name: str, dev: torch.device, param_dtype: str | None = None):
+    spec = dict(WORKLOADS[name])
+    if param_dtype is not None:
+        spec["param"] = spec["grad"] = param_dtype
     shapes = mg.paramsets.WORKLOADS[name]()
     decay = [(n, s) for n, s in shapes if len(s) >= 2]
     nodecay = [(n, s) for n, s in shapes if len(s) < 2]
@@ -118,6 +121,74 @@ def read_traffic(name: str) -> float | None:
     return None
 
 
+def vs_torch(name: str, steps: int, warmup: int, dev: torch.device) -> dict:
+    """The reference's own GPU path on this GPU, beside this package, on the
+    same fp32 parameters and gradients.  On a cuda device the reference's
+    loop builds torch.optim.AdamW(..., fused=True) (train.py:359-365 with
+    src/minigpt/runtime.py:164) and torch.amp.GradScaler('cuda')
+    (train.py:366-370) over fp32 parameters, and calls unscale_ ->
+    clip_grad_norm_ -> step -> update (train.py:485-491).  Gradients are
+    refilled before every step (torch's unscale_ and clip rewrite them in
+    place); HIP events on the current stream bracket only the four calls.
+    The two optimizers keep separate state and update the shared parameters
+    in turn, each for warmup + steps iterations, twice."""
+    _, ordered, params, groups = build_workload(name, dev, param_dtype="f32")
+    n_params = sum(p.numel() for p in params)
+    init_scale = 65536.0
+    stream = torch.cuda.current_stream(dev)
+
+    def refill(step: int) -> None:
+        for i, p in enumerate(params):
+            if p.grad is None:
+                p.grad = torch.empty_like(p)
+            syn.fill_(p.grad, syn.GRAD_SEED, syn.grad_stream(step, i), 1e-3 * init_scale)
+
+    def torch_groups():
+        return [{k: v for k, v in g.items()} for g in groups]
+
+    runs = {
+        "torch": (torch.optim.AdamW(torch_groups(), lr=3e-4, betas=(0.9, 0.95), eps=1e-8, fused=True),
+                  torch.amp.GradScaler("cuda", init_scale=init_scale), torch.nn.utils.clip_grad_norm_),
+        "mgopt": (mg.AdamW(torch_groups(), lr=3e-4, betas=(0.9, 0.95), eps=1e-8),
+                  mg.GradScaler("cuda", init_scale=init_scale), mg.clip_grad_norm_),
+    }
+    ms: dict[str, list[float]] = {k: [] for k in runs}
+    for rnd in range(2):
+        for key, (opt, scaler, clip) in runs.items():
+            scaler.scale(torch.ones((), device=dev))
+            spans = []
+            for s in range(warmup + steps):
+                refill(s + 1)
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                for g in opt.param_groups:
+                    g["lr"] = 3e-4
+                scaler.unscale_(opt)
+                clip(params, 1.0)
+                scaler.step(opt)
+                scaler.update()
+                b.record(stream)
+                if s >= warmup:
+                    spans.append((a, b))
+            torch.cuda.synchronize()
+            ms[key].append(sum(a.elapsed_time(b) for a, b in spans) / len(spans))
+            log(f"round {rnd}: {key} {ms[key][-1]:.3f} ms/step")
+    t, m = min(ms["torch"]), min(ms["mgopt"])
+    return {
+        "comparison": "the reference's GPU optimizer step (torch AdamW fused=True + torch.amp.GradScaler + "
+                      "clip_grad_norm_) vs this package, same GPU, same fp32 params and fp32 grads",
+        "workload": name, "tensors": len(params), "params": n_params, "steps": steps, "warmup": warmup,
+        "torch_version": torch.__version__,
+        "torch_ms_per_step": ms["torch"], "mgopt_ms_per_step": ms["mgopt"],
+        "torch_steps_per_s": 1e3 / t, "mgopt_steps_per_s": 1e3 / m,
+        "speedup": t / m,
+        "compulsory_bytes_per_param": 28,
+        "torch_compulsory_GBps": 28 * n_params / (t * 1e-3) / 1e9,
+        "mgopt_compulsory_GBps": 28 * n_params / (m * 1e-3) / 1e9,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -126,6 +197,9 @@ def main() -> int:
     ap.add_argument("--workload", default="qwen3_8b", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-params", type=int, default=1_000_000_000)
+    ap.add_argument("--vs-torch", action="store_true",
+                    help="instead of the benchmark line, time torch's own GPU path (the reference's fused AdamW + "
+                         "GradScaler + clip_grad_norm_) beside this package on fp32 params and grads of the workload")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB fp32 device copy (reads 1 GiB, writes 1 GiB) three times, "
                          "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -143,6 +217,9 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibration": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30, "launches": 3}))
+        return 0
+    if args.vs_torch:
+        print(json.dumps(vs_torch(args.workload, args.steps, args.warmup, dev)), flush=True)
         return 0
     spec, ordered, params, groups = build_workload(args.workload, dev)
     n_params = sum(p.numel() for p in params)

@@ -66,7 +66,8 @@ def _norm_only(grads: list[torch.Tensor], max_norm: float) -> torch.Tensor:
     return norm
 
 
-@torch.no_grad()
+# (no no_grad wrapper: nothing here records autograd history, the kernels
+# write through raw pointers, and the decorator costs ~2.5 us per call)
 def clip_grad_norm_(
     parameters: torch.Tensor | Iterable[torch.Tensor],
     max_norm: float,

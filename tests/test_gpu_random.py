@@ -52,7 +52,7 @@ def _config(seed: int) -> dict:
         if scaler and r.rand() < 0.6 else {}
     return dict(pdt=pdt, gdt=gdt, groups=groups, sizes=sizes, group_of=group_of, scaler=scaler,
                 max_norm=None if r.rand() < 0.3 else float(r.choice([0.05, 1.0])), steps=steps, bad=bad,
-                chunk=int(r.choice([4096, 8192, 65536])), sigma=float(10.0 ** r.uniform(-3, -1)),
+                chunk=int(r.choice([512, 1024, 4096, 65536])), sigma=float(10.0 ** r.uniform(-3, -1)),
                 lr=float(10.0 ** r.uniform(-4, -2)))
 
 

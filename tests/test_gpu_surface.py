@@ -536,3 +536,42 @@ def test_one_scaler_two_optimizers():
         traj.append(sc.get_scale())
     assert traj == [64.0, 128.0, 64.0, 64.0, 128.0, 128.0]
     assert mg.optimizer_completed_steps(oa) == 6 and mg.optimizer_completed_steps(ob) == 5
+
+
+def test_step_hooks_and_profiler_range_follow_torch():
+    """Pre hooks run global-first and may replace the arguments, post hooks
+    run per-optimizer-first (torch/optim/optimizer.py:503-536), and the step
+    shows up as Optimizer.step#AdamW.step under the profiler."""
+    from torch.optim.optimizer import register_optimizer_step_post_hook, register_optimizer_step_pre_hook
+
+    params = _params([(64, 5)])
+    opt = mg.AdamW(params, lr=1e-3)
+    calls = []
+    closure_calls = []
+
+    def closure():
+        closure_calls.append(torch.is_grad_enabled())
+        return torch.tensor(2.0)
+
+    handles = [
+        register_optimizer_step_pre_hook(lambda o, a, k: calls.append("global pre")),
+        opt.register_step_pre_hook(lambda o, a, k: (calls.append("pre"), ((o,), {"closure": closure}))[1]),
+        opt.register_step_post_hook(lambda o, a, k: calls.append(("post", k.get("closure") is closure))),
+        register_optimizer_step_post_hook(lambda o, a, k: calls.append("global post")),
+    ]
+    try:
+        _grads(params, 1, 0.1)
+        loss = opt.step()
+    finally:
+        for h in handles:
+            h.remove()
+    assert calls == ["global pre", "pre", ("post", True), "global post"]
+    assert closure_calls == [True] and float(loss) == 2.0
+    assert torch.is_grad_enabled()  # the step leaves the caller's grad mode as it was
+
+    with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CPU]) as prof:
+        _grads(params, 2, 0.1)
+        opt.step()
+    torch.cuda.synchronize()
+    assert any(e.name == "Optimizer.step#AdamW.step" for e in prof.events())
+    assert float(opt.state[params[0]]["step"]) == 2.0

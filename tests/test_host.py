@@ -210,3 +210,14 @@ def test_scheduler_helpers(mg):
     mg.set_optimizer_lr(opt, 0.125)
     assert all(g["lr"] == 0.125 for g in opt.param_groups)
     assert mg.optimizer_completed_steps(opt) == 0
+
+
+def test_step_is_wrapped_once_with_torch_hook_semantics(mg):
+    """AdamW.step carries its own hook wrapper (marked hooked), so building
+    optimizers, subclassing and unpickling never wrap it a second time."""
+    raw = mg.AdamW.step.__wrapped__
+    assert mg.AdamW.step.hooked is True
+    mg.AdamW([nn.Parameter(torch.zeros(3))], lr=1e-3)
+    mg.AdamW([nn.Parameter(torch.zeros(3))], lr=1e-3)
+    assert mg.AdamW.step.__wrapped__ is raw
+    assert not hasattr(raw, "__wrapped__")
