@@ -101,12 +101,25 @@ def time_cpu_baseline(name: str, budget_params: int) -> dict:
         "unit": "steps/s",
         "cores": r["threads"],
         "kind": "reference",
+        "cpu_model": cpu_model(),
         "sample": (f"torch {torch.__version__.split('+')[0]} CPU AdamW(fused=False) + clip_grad_norm_ + "
                    f"GradScaler('cpu'), the calls of train.py:485-491, on {r['tensors']} tensors / {r['params']:,} fp32 params "
                    f"of the workload; median of 5 steps = {r['seconds']*1e3:.1f} ms ({ns_per_param:.3f} ns/param: "
                    f"unscale {r['unscale_s']*1e3:.1f} ms, clip {r['clip_s']*1e3:.1f} ms, step {r['step_s']*1e3:.1f} ms, "
                    f"update {r['update_s']*1e3:.2f} ms), extrapolated to {total:,} params"),
     }
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (first entry of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def read_traffic(name: str) -> float | None:

@@ -14,6 +14,7 @@ from __future__ import annotations
 import ctypes
 import types
 import warnings
+import weakref
 from typing import Iterable
 
 import torch
@@ -22,6 +23,7 @@ from . import _native as N
 from .adamw import engine_of
 
 _GRAD_PLANS: dict[tuple, tuple[int, list[int]]] = {}
+_last_fast: tuple[tuple, weakref.ref] | None = None   # (id tuple, engine) of the last fused-path call
 
 
 def _norm_only(grads: list[torch.Tensor], max_norm: float) -> torch.Tensor:
@@ -91,10 +93,18 @@ def clip_grad_norm_(
     max_norm = float(max_norm)
 
     # Fast path: this exact parameter list was seen before and is the whole
-    # parameter set of one optimizer (the train.py:486 call, every step).
+    # parameter set of one optimizer (the train.py:486 call, every step).  The
+    # last such list is remembered with its engine, which holds the
+    # parameters (so their ids cannot be reused while it lives).
+    global _last_fast
     key = tuple(map(id, parameters))
+    if _last_fast is not None and _last_fast[0] == key and (eng := _last_fast[1]()) is not None:
+        total = eng.norm(max_norm)
+        _check_finite(total, error_if_nonfinite)
+        return total
     eng = engine_of(parameters[0]) if parameters else None
     if eng is not None and key in eng.complete_keys:
+        _last_fast = (key, weakref.ref(eng))
         total = eng.norm(max_norm)
         _check_finite(total, error_if_nonfinite)
         return total

@@ -84,6 +84,9 @@ class _Engine:
             if p.dtype not in (torch.float32, torch.float16, torch.bfloat16):
                 raise TypeError(f"unsupported parameter dtype {p.dtype}")
         self.device = dev
+        lib = N.lib()
+        # the two per-iteration entry points, bound once
+        self._grad_norm, self._adamw_step = lib.mgopt_grad_norm, lib.mgopt_adamw_step
         self.chunk_elems = int(chunk_elems or DEFAULT_CHUNK)
         lowp = [p.dtype != torch.float32 for p in self.params]
         if master_weights is False and any(lowp):
@@ -143,9 +146,11 @@ class _Engine:
         self.t_bound = 0                     # upper bound of any step count reachable next step
         self.bc_cap = 0
         self.bc_keys: list[tuple[float, float]] = []
+        self.bc_src: list[tuple] | None = None   # the hp_key the table was last checked against
         self.bc_table: torch.Tensor | None = None
         self.hp = None                       # GroupHparams array passed to mgopt_adamw_step
         self.hp_key: list[tuple] | None = None
+        self.hp_raw: list[tuple] | None = None
         self.reset_iteration()
 
     @property
@@ -315,7 +320,7 @@ class _Engine:
         """max_norm None: no clipping requested, the coefficient is not written."""
         scale = self.scale_src
         N.check(
-            N.lib().mgopt_grad_norm(
+            self._grad_norm(
                 self.plan,
                 scale.data_ptr() if scale is not None else None,
                 float(max_norm) if max_norm is not None else 0.0,
@@ -327,8 +332,11 @@ class _Engine:
             "mgopt_grad_norm",
         )
 
-    def _ensure_bc(self, groups: list[dict[str, Any]]) -> None:
-        keys = [(float(g["betas"][0]), float(g["betas"][1])) for g in groups]
+    def _ensure_bc(self) -> None:
+        """(Re)builds the bias-correction table when the reachable step bound
+        outgrows it or a group's betas changed."""
+        self.bc_src = self.hp_key
+        keys = [(k[2], k[3]) for k in self.hp_key]
         need = self.t_bound + 2
         if self.bc_table is not None and need <= self.bc_cap and keys == self.bc_keys:
             return
@@ -366,24 +374,30 @@ class _Engine:
             if grad_scale is not None:
                 scale = grad_scale
             skip_src = found_inf
-        key = []
-        for g in groups:
-            if g.get("amsgrad", False):
-                raise NotImplementedError("amsgrad is not supported by mgopt AdamW")
-            lr = g["lr"]
-            key.append((float(lr.item() if isinstance(lr, torch.Tensor) else lr), float(g["weight_decay"]),
-                        float(g["betas"][0]), float(g["betas"][1]), float(g["eps"]), bool(g.get("maximize", False))))
-        if key != self.hp_key:
-            # the hyperparameter block is rewritten only when a group changed
-            hp = (N.GroupHparams * len(groups))()
-            for d, (lr, wd, b1, b2, eps, maximize) in zip(hp, key):
-                d.lr, d.weight_decay, d.beta1, d.beta2, d.eps, d.maximize = lr, wd, b1, b2, eps, int(maximize)
-            self.hp, self.hp_key = hp, key
+        # the groups' values as stored: compared as they are, converted and
+        # checked only when one changed (a tensor lr is always re-read)
+        raw = [(g["lr"], g["weight_decay"], g["betas"], g["eps"], g.get("maximize", False), g.get("amsgrad", False))
+               for g in groups]
+        if any(isinstance(r[0], torch.Tensor) for r in raw) or raw != self.hp_raw:
+            key = []
+            for lr, wd, betas, eps, maximize, amsgrad in raw:
+                if amsgrad:
+                    raise NotImplementedError("amsgrad is not supported by mgopt AdamW")
+                key.append((float(lr.item() if isinstance(lr, torch.Tensor) else lr), float(wd),
+                            float(betas[0]), float(betas[1]), float(eps), bool(maximize)))
+            if key != self.hp_key:
+                # the hyperparameter block is rewritten only when a group changed
+                hp = (N.GroupHparams * len(groups))()
+                for d, (lr, wd, b1, b2, eps, maximize) in zip(hp, key):
+                    d.lr, d.weight_decay, d.beta1, d.beta2, d.eps, d.maximize = lr, wd, b1, b2, eps, int(maximize)
+                self.hp, self.hp_key = hp, key
+            self.hp_raw = None if any(isinstance(r[0], torch.Tensor) for r in raw) else raw
         self.t_bound += 1
-        self._ensure_bc(groups)
+        if self.t_bound + 2 > self.bc_cap or self.bc_src is not self.hp_key:
+            self._ensure_bc()
         flags = N.WRITEBACK_GRADS if writeback else 0
         N.check(
-            N.lib().mgopt_adamw_step(
+            self._adamw_step(
                 self.plan, self.hp, self.bc_table.data_ptr(), self.bc_cap,
                 scale.data_ptr() if scale is not None else None,
                 self.coef.data_ptr() if self.clip_pending else None,
