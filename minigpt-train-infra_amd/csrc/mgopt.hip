@@ -23,6 +23,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -57,6 +58,12 @@ constexpr bool kNtNormLoad = true;   // nontemporal gradient loads in pass 1
 // work-groups per class measured 0.1-0.15 ms slower per step on the Qwen3-8B
 // set than 64K elements per work-group.)
 constexpr int64_t kNormChunk = 65536;
+// A dispatch packet carries its grid size in work-items as a 32-bit value, so
+// launches over more chunks than this are issued in pieces, each piece given
+// its first chunk (and first partial slot) as arguments.  2^22 work-groups of
+// 512 threads are 2^31 work-items; at 1024-element chunks one piece covers
+// 4.3e9 elements.
+constexpr uint32_t kMaxGroupsPerLaunch = 1u << 22;
 // The command processor hands work-groups to the 8 XCDs round-robin in
 // blockIdx order.  With the remap each XCD instead walks one contiguous range
 // of chunks, so its L2 and address-translation caches see 1/8 of the address
@@ -842,16 +849,28 @@ int launch_check(const char* what) {
 
 template <typename GT>
 int launch_norm(const mgopt_plan* P, const mgopt_plan::Class& c, const float* scale, hipStream_t s) {
-    NormArgs a{P->d_tensors, P->d_norm_chunks, P->d_grads, P->d_partials, scale, kNormChunk, c.norm_begin, c.norm_count,
-               c.partial_base};
-    hipLaunchKernelGGL(norm_kernel<GT>, dim3(c.norm_count), dim3(kBlock), 0, s, a);
-    return launch_check("norm_kernel");
+    // partial slot = partial_base + chunk position, so the pieces fill the
+    // class's partials exactly as one launch would
+    for (uint64_t done = 0; done < c.norm_count; done += kMaxGroupsPerLaunch) {
+        const uint32_t n = static_cast<uint32_t>(std::min<uint64_t>(c.norm_count - done, kMaxGroupsPerLaunch));
+        NormArgs a{P->d_tensors, P->d_norm_chunks, P->d_grads, P->d_partials, scale, kNormChunk,
+                   static_cast<uint32_t>(c.norm_begin + done), n, static_cast<uint32_t>(c.partial_base + done)};
+        hipLaunchKernelGGL(norm_kernel<GT>, dim3(n), dim3(kBlock), 0, s, a);
+        if (int rc = launch_check("norm_kernel")) return rc;
+    }
+    return 0;
 }
 
 template <typename GT, int LOWP>
-int launch_adamw(const AdamArgs& a, uint32_t count, hipStream_t s) {
-    hipLaunchKernelGGL((adamw_kernel<GT, LOWP>), dim3(count), dim3(kAdamBlock), kAdamLds, s, a);
-    return launch_check("adamw_kernel");
+int launch_adamw(AdamArgs a, uint32_t count, hipStream_t s) {
+    const uint32_t begin = a.chunk_begin;
+    for (uint64_t done = 0; done < count; done += kMaxGroupsPerLaunch) {
+        const uint32_t n = static_cast<uint32_t>(std::min<uint64_t>(count - done, kMaxGroupsPerLaunch));
+        a.chunk_begin = static_cast<uint32_t>(begin + done);
+        hipLaunchKernelGGL((adamw_kernel<GT, LOWP>), dim3(n), dim3(kAdamBlock), kAdamLds, s, a);
+        if (int rc = launch_check("adamw_kernel")) return rc;
+    }
+    return 0;
 }
 
 template <typename GT>
@@ -1126,22 +1145,25 @@ MGOPT_API int mgopt_scale_grads(mgopt_plan* P, const float* coef_dev, void* stre
     DeviceGuard guard(P->device);
     hipStream_t s = static_cast<hipStream_t>(stream);
     for (const auto& c : P->classes) {
-        switch (c.grad_dtype) {
-            case MGOPT_F32:
-                hipLaunchKernelGGL(scale_grads_kernel<float>, dim3(c.count), dim3(kBlock), 0, s, P->d_tensors, P->d_chunks,
-                                   P->d_grads, coef_dev, P->chunk_elems, c.begin);
-                break;
-            case MGOPT_F16:
-                hipLaunchKernelGGL(scale_grads_kernel<_Float16>, dim3(c.count), dim3(kBlock), 0, s, P->d_tensors,
-                                   P->d_chunks, P->d_grads, coef_dev, P->chunk_elems, c.begin);
-                break;
-            case MGOPT_BF16:
-                hipLaunchKernelGGL(scale_grads_kernel<Bf16>, dim3(c.count), dim3(kBlock), 0, s, P->d_tensors, P->d_chunks,
-                                   P->d_grads, coef_dev, P->chunk_elems, c.begin);
-                break;
-            default: return fail(MGOPT_E_INVALID, "bad grad dtype");
+        for (uint64_t done = 0; done < c.count; done += kMaxGroupsPerLaunch) {
+            const uint32_t n = static_cast<uint32_t>(std::min<uint64_t>(c.count - done, kMaxGroupsPerLaunch));
+            switch (c.grad_dtype) {
+                case MGOPT_F32:
+                    hipLaunchKernelGGL(scale_grads_kernel<float>, dim3(n), dim3(kBlock), 0, s, P->d_tensors, P->d_chunks,
+                                       P->d_grads, coef_dev, P->chunk_elems, static_cast<uint32_t>(c.begin + done));
+                    break;
+                case MGOPT_F16:
+                    hipLaunchKernelGGL(scale_grads_kernel<_Float16>, dim3(n), dim3(kBlock), 0, s, P->d_tensors,
+                                       P->d_chunks, P->d_grads, coef_dev, P->chunk_elems, static_cast<uint32_t>(c.begin + done));
+                    break;
+                case MGOPT_BF16:
+                    hipLaunchKernelGGL(scale_grads_kernel<Bf16>, dim3(n), dim3(kBlock), 0, s, P->d_tensors, P->d_chunks,
+                                       P->d_grads, coef_dev, P->chunk_elems, static_cast<uint32_t>(c.begin + done));
+                    break;
+                default: return fail(MGOPT_E_INVALID, "bad grad dtype");
+            }
+            if (int rc = launch_check("scale_grads_kernel")) return rc;
         }
-        if (int rc = launch_check("scale_grads_kernel")) return rc;
     }
     return 0;
 }
@@ -1152,15 +1174,17 @@ MGOPT_API int mgopt_sync_master(mgopt_plan* P, void* stream) {
     DeviceGuard guard(P->device);
     hipStream_t s = static_cast<hipStream_t>(stream);
     for (const auto& c : P->classes) {
-        if (c.lowp_dtype == MGOPT_BF16)
-            hipLaunchKernelGGL(sync_master_kernel<Bf16>, dim3(c.count), dim3(kBlock), 0, s, P->d_tensors, P->d_chunks,
-                               P->chunk_elems, c.begin);
-        else if (c.lowp_dtype == MGOPT_F16)
-            hipLaunchKernelGGL(sync_master_kernel<_Float16>, dim3(c.count), dim3(kBlock), 0, s, P->d_tensors, P->d_chunks,
-                               P->chunk_elems, c.begin);
-        else
-            continue;
-        if (int rc = launch_check("sync_master_kernel")) return rc;
+        if (c.lowp_dtype != MGOPT_BF16 && c.lowp_dtype != MGOPT_F16) continue;
+        for (uint64_t done = 0; done < c.count; done += kMaxGroupsPerLaunch) {
+            const uint32_t n = static_cast<uint32_t>(std::min<uint64_t>(c.count - done, kMaxGroupsPerLaunch));
+            if (c.lowp_dtype == MGOPT_BF16)
+                hipLaunchKernelGGL(sync_master_kernel<Bf16>, dim3(n), dim3(kBlock), 0, s, P->d_tensors, P->d_chunks,
+                                   P->chunk_elems, static_cast<uint32_t>(c.begin + done));
+            else
+                hipLaunchKernelGGL(sync_master_kernel<_Float16>, dim3(n), dim3(kBlock), 0, s, P->d_tensors, P->d_chunks,
+                                   P->chunk_elems, static_cast<uint32_t>(c.begin + done));
+            if (int rc = launch_check("sync_master_kernel")) return rc;
+        }
     }
     return 0;
 }

@@ -61,6 +61,16 @@ def _check_full(pair: Pair, label: str, expect_steps: int) -> None:
         f"subset of {len(pair.case.subset)} tensors bit-exact")
 
 
+def _tensor_at_chunk(shapes_in_plan_order, chunk_elems: int, chunk: int) -> int:
+    """Position of the tensor that holds pass-2 chunk number `chunk`."""
+    seen = 0
+    for k, s in enumerate(shapes_in_plan_order):
+        seen += -(-math.prod(s) // chunk_elems)
+        if seen > chunk:
+            return k
+    raise ValueError("the set has fewer chunks")
+
+
 def _run_with_skip_check(pair: Pair, steps: int, skip_step: int) -> None:
     c = pair.case
     for s in range(1, steps + 1):
@@ -118,8 +128,12 @@ def test_qwen3_8b_full_size():
     step 2 (a skipped step over the whole set)."""
     shapes = mg.paramsets.WORKLOADS["qwen3_8b"]()
     decay_n = sum(1 for _, s in shapes if len(s) >= 2)
-    subset = [1, 2, 5, decay_n - 2] + list(range(decay_n, len(shapes)))
-    log("case: qwen3_8b full size, 4 steps, inf at step 2")
+    # pass 2 runs over 8.0M chunks in two launches of at most 2^22 work-groups:
+    # the tensor that holds the first chunk of the second launch is checked too
+    straddle = _tensor_at_chunk([s for _, s in shapes if len(s) >= 2] + [s for _, s in shapes if len(s) < 2],
+                                mg.engine.DEFAULT_CHUNK, 1 << 22)
+    subset = sorted({1, 2, 5, straddle, decay_n - 2}) + list(range(decay_n, len(shapes)))
+    log(f"case: qwen3_8b full size, 4 steps, inf at step 2, launch-piece boundary in tensor {straddle}")
     pair = Pair(Case(shapes=shapes, param_dtype="bf16", grad_dtype="bf16", steps=4, sigma=1e-3,
                      scaler=dict(init_scale=65536.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=2000),
                      inject={2: [(7, 123, float("inf"))]}, subset=subset, fresh_grads=False))
