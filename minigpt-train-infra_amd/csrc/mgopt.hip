@@ -59,11 +59,12 @@ constexpr bool kNtNormLoad = true;   // nontemporal gradient loads in pass 1
 // set than 64K elements per work-group.)
 constexpr int64_t kNormChunk = 65536;
 // A dispatch packet carries its grid size in work-items as a 32-bit value, so
-// launches over more chunks than this are issued in pieces, each piece given
-// its first chunk (and first partial slot) as arguments.  2^22 work-groups of
-// 512 threads are 2^31 work-items; at 1024-element chunks one piece covers
-// 4.3e9 elements.
-constexpr uint32_t kMaxGroupsPerLaunch = 1u << 22;
+// launches over more chunks than fit are issued in pieces, each piece given
+// its first chunk (and first partial slot) as arguments.  8,388,607
+// work-groups of 512 threads are the most one packet holds; at 1024-element
+// chunks one piece covers 8.59e9 elements.
+constexpr uint32_t kMaxGroupsPerLaunch = 0xFFFFFFFFu / 512;
+static_assert(kBlock <= 512 && kAdamBlock <= 512, "kMaxGroupsPerLaunch assumes work-groups of at most 512 threads");
 // The command processor hands work-groups to the 8 XCDs round-robin in
 // blockIdx order.  With the remap each XCD instead walks one contiguous range
 // of chunks, so its L2 and address-translation caches see 1/8 of the address

@@ -128,18 +128,31 @@ def test_qwen3_8b_full_size():
     step 2 (a skipped step over the whole set)."""
     shapes = mg.paramsets.WORKLOADS["qwen3_8b"]()
     decay_n = sum(1 for _, s in shapes if len(s) >= 2)
-    # pass 2 runs over 8.0M chunks in two launches of at most 2^22 work-groups:
-    # the tensor that holds the first chunk of the second launch is checked too
-    straddle = _tensor_at_chunk([s for _, s in shapes if len(s) >= 2] + [s for _, s in shapes if len(s) < 2],
-                                mg.engine.DEFAULT_CHUNK, 1 << 22)
-    subset = sorted({1, 2, 5, straddle, decay_n - 2}) + list(range(decay_n, len(shapes)))
-    log(f"case: qwen3_8b full size, 4 steps, inf at step 2, launch-piece boundary in tensor {straddle}")
+    subset = [1, 2, 5, decay_n - 2] + list(range(decay_n, len(shapes)))
+    log("case: qwen3_8b full size, 4 steps, inf at step 2")
     pair = Pair(Case(shapes=shapes, param_dtype="bf16", grad_dtype="bf16", steps=4, sigma=1e-3,
                      scaler=dict(init_scale=65536.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=2000),
                      inject={2: [(7, 123, float("inf"))]}, subset=subset, fresh_grads=False))
     _run_with_skip_check(pair, 4, skip_step=2)
     assert [o["skipped"] for o in pair.outs] == [False, True, False, False]
     _check_full(pair, "qwen3_8b", 3)
+
+
+def test_pass2_beyond_one_dispatch():
+    """4.43e9 elements in 512-element chunks: 8,650,752 pass-2 work-groups,
+    more than one dispatch packet's 32-bit work-item count holds at 512
+    threads (8,388,607 work-groups), so pass 2 runs in two launches.  The
+    tensor holding the first chunk of the second launch, and the first and
+    last tensors, are checked bit for bit against the oracle; every step count
+    and the error flag cover the rest.  fp32 params, fp16 grads, 62 GB."""
+    shapes = [(f"w{i}", (4096, 4096)) for i in range(264)]
+    boundary = _tensor_at_chunk([s for _, s in shapes], 512, 0xFFFFFFFF // 512)
+    subset = sorted({0, boundary, len(shapes) - 1})
+    log(f"case: 264 x 4096x4096 fp32/fp16, chunk 512, 2 steps, second launch starts in tensor {boundary}")
+    pair = Pair(Case(shapes=shapes, param_dtype="f32", grad_dtype="f16", steps=2, sigma=1e-3, scaler=None,
+                     subset=subset, chunk_elems=512))
+    pair.run()
+    _check_full(pair, "two dispatches", 2)
 
 
 def test_ragged_full_size():
