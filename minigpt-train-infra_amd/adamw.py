@@ -207,6 +207,7 @@ class AdamW(torch.optim.Optimizer):
         """Copies state entries a caller assigned directly into the arenas."""
         eng = self._get_engine()
         self._sync_all_masters()
+        changed = []
         for i, p in enumerate(eng.params):
             entry = dict.get(self.state, p)
             views = eng.views[i]
@@ -220,27 +221,57 @@ class AdamW(torch.optim.Optimizer):
                 continue
             if all(entry.get(k) is views[k] for k in ("step", "exp_avg", "exp_avg_sq")):
                 continue
-            self._copy_in(i, entry)
+            changed.append((i, entry))
+        self._copy_in_many(changed)
         self._install_views(only_existing=True)
         eng.t_bound = max(eng.t_bound, int(eng.steps.max().item()) if len(eng.params) else 0)
         self._state_dirty = False
 
-    def _copy_in(self, i: int, entry: dict[str, Any]) -> None:
+    def _copy_in_many(self, items: list[tuple[int, dict[str, Any]]]) -> None:
+        """Copies saved per-parameter state into the arenas: every step count
+        in one indexed write (no per-parameter .item(), which would wait for
+        the GPU when the saved steps live there) and the moments and masters
+        in multi-tensor copies (a few launches instead of two or three per
+        parameter).  Missing moments start from zero."""
+        if not items:
+            return
         eng = self._get_engine()
-        views = eng.views[i]
-        step = entry.get("step", 0.0)
-        views["step"].fill_(float(step.item()) if isinstance(step, torch.Tensor) else float(step))
-        for key in ("exp_avg", "exp_avg_sq"):
-            src = entry.get(key)
-            if src is None:
-                views[key].zero_()
+        host_idx: list[int] = []
+        host_val: list[float] = []
+        dev_idx: list[int] = []
+        dev_val: list[torch.Tensor] = []
+        dst: list[torch.Tensor] = []
+        src: list[torch.Tensor] = []
+        zero: list[torch.Tensor] = []
+        for i, entry in items:
+            views = eng.views[i]
+            step = entry.get("step", 0.0)
+            if isinstance(step, torch.Tensor) and step.device.type != "cpu":
+                dev_idx.append(i)
+                dev_val.append(step.reshape(()).to(torch.float32))
             else:
-                if src.numel() != views[key].numel():
-                    raise ValueError(f"state {key} of parameter {i} has {src.numel()} elements, expected {views[key].numel()}")
-                views[key].copy_(src.reshape(views[key].shape))
-        if "master_param" in views and entry.get("master_param") is not None:
-            views["master_param"].copy_(entry["master_param"].reshape(views["master_param"].shape))
-        self._installed.add(i)
+                host_idx.append(i)
+                host_val.append(float(step))
+            keys = ["exp_avg", "exp_avg_sq"] + (["master_param"] if "master_param" in views else [])
+            for key in keys:
+                t = entry.get(key)
+                if t is None:
+                    if key != "master_param":
+                        zero.append(views[key])
+                    continue
+                if t.numel() != views[key].numel():
+                    raise ValueError(f"state {key} of parameter {i} has {t.numel()} elements, expected {views[key].numel()}")
+                dst.append(views[key])
+                src.append(t.reshape(views[key].shape))
+        if host_idx:
+            eng.steps[torch.tensor(host_idx, device=eng.device)] = torch.tensor(host_val, dtype=torch.float32).to(eng.device)
+        if dev_idx:
+            eng.steps[torch.tensor(dev_idx, device=eng.device)] = torch.stack(dev_val).to(eng.device)
+        if zero:
+            torch._foreach_zero_(zero)
+        if dst:
+            torch._foreach_copy_(dst, src)
+        self._installed.update(i for i, _ in items)
 
     def _sync_all_masters(self) -> None:
         """Master copies start from the current bf16/fp16 parameters; saved
@@ -393,18 +424,19 @@ class AdamW(torch.optim.Optimizer):
                 ng["param_names"] = g["param_names"]
             new_groups.append(ng)
         self.param_groups = new_groups
-        # loading replaces all state: parameters absent from the saved state start fresh
-        eng.exp_avg.zero_()
-        eng.exp_avg_sq.zero_()
+        # loading replaces all state: parameters absent from the saved state
+        # start fresh (their moment segments are zeroed; the others are
+        # overwritten by the copy)
+        items = [(index[id(id_to_param[pid])], entry) for pid, entry in state_dict["state"].items() if pid in id_to_param]
+        present = {i for i, _ in items}
+        fresh = [eng.views[i][k] for i in range(len(eng.params)) if i not in present for k in ("exp_avg", "exp_avg_sq")]
+        if fresh:
+            torch._foreach_zero_(fresh)
         eng.steps.zero_()
         self._installed.clear()
         eng.master_synced = False
         self._sync_all_masters()
-        for pid, entry in state_dict["state"].items():
-            p = id_to_param.get(pid)
-            if p is None:
-                continue
-            self._copy_in(index[id(p)], entry)
+        self._copy_in_many(items)
         dict.clear(self.state)
         self._install_views(only_existing=True)
         eng.t_bound = int(eng.steps.max().item())

@@ -575,3 +575,37 @@ def test_step_hooks_and_profiler_range_follow_torch():
     torch.cuda.synchronize()
     assert any(e.name == "Optimizer.step#AdamW.step" for e in prof.events())
     assert float(opt.state[params[0]]["step"]) == 2.0
+
+
+def test_loading_a_partial_state_resets_the_absent_parameters():
+    """load_state_dict replaces all state (torch/optim/optimizer.py:677-767):
+    a parameter absent from the loaded state starts fresh (zero moments, step
+    0) even after steps, while the present ones take the loaded values; steps
+    saved on the GPU and on the CPU both load."""
+    params = _params([(64, 33), (100,), (7, 9)])
+    opt = mg.AdamW(params, lr=1e-3)
+    for s in range(1, 4):
+        _grads(params, s, 0.1)
+        opt.step()
+    sd = opt.state_dict()
+    saved = {k: {n: t.clone() for n, t in v.items()} for k, v in sd["state"].items()}
+    partial = {"state": {0: saved[0], 2: {**saved[2], "step": saved[2]["step"].cpu()}},
+               "param_groups": sd["param_groups"]}
+    for s in range(4, 6):
+        _grads(params, s, 0.1)
+        opt.step()
+    opt.load_state_dict(partial)
+    torch.cuda.synchronize()
+    for i in (0, 2):
+        st = opt.state[params[i]]
+        assert float(st["step"]) == 3.0
+        for k in ("exp_avg", "exp_avg_sq"):
+            assert torch.equal(st[k], saved[i][k]), (i, k)
+    assert params[1] not in opt.state
+    eng = opt._engine
+    assert float(eng.steps[1]) == 0.0
+    assert not bool(eng.views[1]["exp_avg"].any()) and not bool(eng.views[1]["exp_avg_sq"].any())
+    _grads(params, 6, 0.1)
+    opt.step()
+    torch.cuda.synchronize()
+    assert [float(opt.state[p]["step"]) for p in params] == [4.0, 1.0, 4.0]
