@@ -389,12 +389,34 @@ class AdamW(torch.optim.Optimizer):
         self._get_engine().sync_master()
 
     def add_param_group(self, param_group: dict[str, Any]) -> None:
-        if getattr(self, "_engine", None) is not None:
-            raise RuntimeError("add_param_group after the first step is not supported; build the optimizer with all groups")
+        old = getattr(self, "_engine", None)
+        if old is not None and (getattr(self, "_grad_arena", None) is not None or old.grad_source is not None):
+            raise RuntimeError("add_param_group after use_grad_arena or set_grad_source is not supported: "
+                               "those gradient buffers are laid out for the current parameters")
         super().add_param_group(param_group)
         me = weakref.ref(self)
         for p in self.param_groups[-1]["params"]:
             _OWNER[p] = me
+        if old is not None:
+            self._rebuild_engine(old)
+
+    @torch.no_grad()
+    def _rebuild_engine(self, old: _Engine) -> None:
+        """A new engine over the enlarged parameter list (arenas are laid out
+        per parameter list).  The new group comes last, so every existing
+        parameter keeps its position; its moments, master copy and step count,
+        and the window record, are copied over exactly."""
+        self._engine = old                       # state assigned since the last step lands in the old arenas first
+        if self._state_dirty:
+            self._reconcile_state()
+        self._engine = None
+        new = self._get_engine()
+        self._sync_all_masters()                 # the new parameters' masters from their values
+        self._copy_in_many([(i, old.views[i]) for i in sorted(self._installed)])
+        new.window.copy_(old.window)
+        new.t_bound = old.t_bound
+        self._install_views(only_existing=True)
+        old.close()
 
     def state_dict(self) -> dict[str, Any]:
         if self._state_dirty:

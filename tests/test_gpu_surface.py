@@ -538,6 +538,7 @@ def test_one_scaler_two_optimizers():
     assert mg.optimizer_completed_steps(oa) == 6 and mg.optimizer_completed_steps(ob) == 5
 
 
+@pytest.mark.filterwarnings("ignore:Warning. Profiler clears events")
 def test_step_hooks_and_profiler_range_follow_torch():
     """Pre hooks run global-first and may replace the arguments, post hooks
     run per-optimizer-first (torch/optim/optimizer.py:503-536), and the step
@@ -609,3 +610,69 @@ def test_loading_a_partial_state_resets_the_absent_parameters():
     opt.step()
     torch.cuda.synchronize()
     assert [float(opt.state[p]["step"]) for p in params] == [4.0, 1.0, 4.0]
+
+
+def test_add_param_group_after_steps_matches_torch():
+    """torch.optim.Optimizer.add_param_group after the first step: the
+    existing parameters keep their state, the new group starts fresh, and the
+    run follows torch's own CPU AdamW (same calls) within the state
+    tolerance."""
+    shapes_a, shapes_b = [(40, 30), (30,)], [(25, 9), (77,)]
+    init = [O.synth(int(np.prod(s)), 1, i, O.synth_k(0.02)).reshape(s) for i, s in enumerate(shapes_a + shapes_b)]
+    cpu = [torch.nn.Parameter(torch.from_numpy(x.copy())) for x in init]
+    gpu = [torch.nn.Parameter(torch.from_numpy(x.copy()).to(DEV)) for x in init]
+    topt = torch.optim.AdamW([{"params": cpu[:2], "weight_decay": 0.1}], lr=1e-3, betas=(0.9, 0.95), fused=False)
+    opt = mg.AdamW([{"params": gpu[:2], "weight_decay": 0.1}], lr=1e-3, betas=(0.9, 0.95))
+    grads = lambda s, n: [O.synth(int(np.prod(sh)), 2, (s << 20) | i, O.synth_k(1e-2)).reshape(sh)
+                          for i, sh in enumerate((shapes_a + shapes_b)[:n])]
+    for s in range(1, 7):
+        if s == 4:
+            for o, ps in ((topt, cpu), (opt, gpu)):
+                o.add_param_group({"params": ps[2:], "weight_decay": 0.0, "group_name": "late"})
+        n = 2 if s < 4 else 4
+        for p, q, g in zip(cpu[:n], gpu[:n], grads(s, n)):
+            p.grad = torch.from_numpy(g)
+            q.grad = torch.from_numpy(g).to(DEV)
+        topt.step()
+        opt.step()
+    torch.cuda.synchronize()
+    assert opt.param_groups[1]["group_name"] == "late"
+    assert [float(opt.state[q]["step"]) for q in gpu] == [6.0, 6.0, 3.0, 3.0]
+    for p, q in zip(cpu, gpu):
+        assert maxrel(q.detach().cpu().numpy(), p.detach().numpy()) <= RTOL_STATE
+        for k in ("exp_avg", "exp_avg_sq"):
+            assert maxrel(opt.state[q][k].cpu().numpy(), topt.state[p][k].numpy()) <= RTOL_STATE
+    assert opt._engine.error_flag() == 0
+
+
+def test_add_param_group_keeps_bf16_masters_bit_exact():
+    """With bf16 parameters the carried-over state includes the fp32 masters:
+    adding a group after three steps equals, bit for bit, an optimizer built
+    with both groups whose late parameters had no gradients for those steps."""
+    shapes = [(64, 48), (48,), (33, 7), (91,)]
+
+    def make():
+        return _params(shapes, torch.bfloat16)
+
+    pa, pb = make(), make()
+    late = mg.AdamW([{"params": pa[:2], "weight_decay": 0.1}], lr=1e-3)
+    full = mg.AdamW([{"params": pb[:2], "weight_decay": 0.1}, {"params": pb[2:], "weight_decay": 0.0}], lr=1e-3)
+    for s in range(1, 7):
+        if s == 4:
+            late.add_param_group({"params": pa[2:], "weight_decay": 0.0})
+        n = 2 if s < 4 else 4
+        _grads(pa[:n], s, 0.05)
+        _grads(pb[:n], s, 0.05)
+        for p in pb[n:]:
+            p.grad = None
+        # the parameters with gradients: each optimizer's whole set with grads,
+        # so both take the fused clip
+        mg.clip_grad_norm_(pa[:n], 1.0)
+        late.step()
+        mg.clip_grad_norm_(pb[:n], 1.0)
+        full.step()
+    torch.cuda.synchronize()
+    for x, y in zip(pa, pb):
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+        for k in ("step", "exp_avg", "exp_avg_sq", "master_param"):
+            assert torch.equal(late.state[x][k], full.state[y][k]), k
