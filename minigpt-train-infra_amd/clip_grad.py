@@ -26,7 +26,7 @@ _GRAD_PLANS: dict[tuple, tuple[int, list[int]]] = {}
 _last_fast: tuple[tuple, weakref.ref] | None = None   # (id tuple, engine) of the last fused-path call
 
 
-def _norm_only(grads: list[torch.Tensor], max_norm: float) -> torch.Tensor:
+def _norm_only(grads: list[torch.Tensor], max_norm: float, error_if_nonfinite: bool) -> torch.Tensor:
     dev = grads[0].device
     if dev.type != "cuda":
         raise RuntimeError("clip_grad_norm_ runs on the GPU only; there is no CPU path")
@@ -64,6 +64,8 @@ def _norm_only(grads: list[torch.Tensor], max_norm: float) -> torch.Tensor:
                             ctypes.c_void_p(coef.data_ptr()), None, stream),
         "mgopt_grad_norm",
     )
+    # torch checks finiteness (clip_grad.py:110-116) before it scales (:232)
+    _check_finite(norm, error_if_nonfinite)
     N.check(lib.mgopt_scale_grads(plan, ctypes.c_void_p(coef.data_ptr()), stream), "mgopt_scale_grads")
     return norm
 
@@ -100,13 +102,13 @@ def clip_grad_norm_(
     key = tuple(map(id, parameters))
     if _last_fast is not None and _last_fast[0] == key and (eng := _last_fast[1]()) is not None:
         total = eng.norm(max_norm)
-        _check_finite(total, error_if_nonfinite)
+        _check_finite(total, error_if_nonfinite, eng)
         return total
     eng = engine_of(parameters[0]) if parameters else None
     if eng is not None and key in eng.complete_keys:
         _last_fast = (key, weakref.ref(eng))
         total = eng.norm(max_norm)
-        _check_finite(total, error_if_nonfinite)
+        _check_finite(total, error_if_nonfinite, eng)
         return total
 
     engines = {id(e): e for p in parameters if (e := engine_of(p)) is not None}
@@ -122,7 +124,7 @@ def clip_grad_norm_(
             if given == {id(p) for p in eng.params} and len(eng.complete_keys) < 8:
                 eng.complete_keys.add(key)
             total = eng.norm(max_norm)
-            _check_finite(total, error_if_nonfinite)
+            _check_finite(total, error_if_nonfinite, eng)
             return total
     for e in engines.values():
         if e.scale_src is not None:
@@ -133,13 +135,15 @@ def clip_grad_norm_(
     grads = [p.grad for p in parameters if p.grad is not None]
     if not grads:
         return torch.tensor(0.0)
-    total = _norm_only(grads, max_norm)
-    _check_finite(total, error_if_nonfinite)
-    return total
+    return _norm_only(grads, max_norm, error_if_nonfinite)
 
 
-def _check_finite(total: torch.Tensor, error_if_nonfinite: bool) -> None:
+def _check_finite(total: torch.Tensor, error_if_nonfinite: bool, eng=None) -> None:
     if error_if_nonfinite and not bool(torch.isfinite(total)):
+        if eng is not None:
+            # torch raises before clipping, so a step taken anyway uses the
+            # unclipped gradients: withdraw the pending coefficient
+            eng.clip_pending = False
         raise RuntimeError(
             "The total norm of order 2.0 for gradients from `parameters` is non-finite, so it cannot be "
             "clipped. To disable this error and scale the gradients by the non-finite norm anyway, "

@@ -70,6 +70,42 @@ def test_writeback_grads_stores_the_clipped_gradient():
         assert np.array_equal(p.grad.cpu().numpy().view(np.uint32), u.view(np.uint32))
 
 
+@pytest.mark.parametrize("pdt,gdt", [("bf16", "bf16"), ("f32", "f16")])
+def test_writeback_grads_in_16_bit_types(pdt, gdt):
+    """writeback_grads with bf16 gradients (bf16 params, fp32 master) and with
+    an fp16 gradient source (fp32 params): each gradient becomes the
+    round-to-nearest-even image of its fp32 unscaled, clipped value."""
+    DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+    params = _params([(300, 11), (4099,)], DT[pdt])
+    opt = mg.AdamW(params, lr=1e-3, writeback_grads=True)
+    grads = [torch.empty(p.shape, dtype=DT[gdt], device=DEV) for p in params]
+    for i, g in enumerate(grads):
+        syn.fill_(g, syn.GRAD_SEED, syn.grad_stream(1, i), 0.3 * 256.0)
+    if pdt == gdt:
+        for p, g in zip(params, grads):
+            p.grad = g
+    else:
+        opt.set_grad_source(grads)
+    sc = mg.GradScaler("cuda", init_scale=256.0)
+    sc.scale(torch.ones((), device=DEV))
+    host = [to_f32(*host_grad(g)) for g in grads]
+    sc.unscale_(opt)
+    norm = mg.clip_grad_norm_(params, 1.0)
+    sc.step(opt)
+    sc.update()
+    torch.cuda.synchronize()
+    inv = O.inv_scale(256.0)
+    un = [O.unscale(h, inv)[0] for h in host]
+    n = O.norm_from_sumsq(O.total_sumsq(un))
+    assert float(norm) == n and n > 1.0
+    coef = O.clip_coef(n, 1.0)
+    for u, g in zip(un, grads):
+        O.scale_(u, coef)
+        want = O.to_bf16(u) if gdt == "bf16" else O.to_f16(u)
+        got = g.detach().view(torch.int16).cpu().numpy().view(np.uint16).ravel()
+        assert np.array_equal(got, want)
+
+
 def test_standalone_clip_matches_torch_semantics():
     """A parameter list no optimizer owns: norm, then grads scaled in place."""
     params = _params([(64, 65), (3,), (100003,)])
@@ -676,3 +712,56 @@ def test_add_param_group_keeps_bf16_masters_bit_exact():
         assert torch.equal(x.view(torch.int16), y.view(torch.int16))
         for k in ("step", "exp_avg", "exp_avg_sq", "master_param"):
             assert torch.equal(late.state[x][k], full.state[y][k]), k
+
+
+def test_clip_grad_norm_arguments_follow_torch():
+    """error_if_nonfinite raises on an inf norm as torch does (and not on a
+    finite one), a bare tensor is accepted, an empty generator warns and
+    gives 0, norm types other than 2 are refused."""
+    params = _params([(40, 7), (13,)])
+    opt = mg.AdamW(params, lr=1e-3)
+    _grads(params, 1, 0.1)
+    n = mg.clip_grad_norm_(params, 1.0, error_if_nonfinite=True)
+    opt.step()
+    _grads(params, 2, 0.1)
+    params[1].grad[3] = float("inf")
+    with pytest.raises(RuntimeError, match="non-finite"):
+        mg.clip_grad_norm_(params, 1.0, error_if_nonfinite=True)
+    t = torch.nn.Parameter(torch.ones(5, device=DEV))
+    t.grad = torch.full((5,), 2.0, device=DEV)
+    assert abs(float(mg.clip_grad_norm_(t, 100.0)) - 20.0 ** 0.5) < 1e-6
+    with pytest.warns(UserWarning, match="empty generator"):
+        assert float(mg.clip_grad_norm_((p for p in []), 1.0)) == 0.0
+    with pytest.raises(NotImplementedError):
+        mg.clip_grad_norm_(params, 1.0, norm_type=1.0)
+    assert float(n) > 0.0
+
+
+def test_nonfinite_error_leaves_gradients_unclipped():
+    """torch raises on a non-finite norm before clipping: the optimizer's own
+    parameters then step with the unclipped gradients, and a parameter list
+    no optimizer owns keeps its gradients untouched."""
+    params = _params([(64, 9), (21,)])
+    opt = mg.AdamW(params, lr=1e-3)
+    ref_params = _params([(64, 9), (21,)])
+    ref = mg.AdamW(ref_params, lr=1e-3)
+    _grads(params, 1, 0.5)
+    _grads(ref_params, 1, 0.5)
+    # a parameter no optimizer owns: the error comes before its gradient is scaled
+    stray = torch.nn.Parameter(torch.zeros(8, device=DEV))
+    stray.grad = torch.full((8,), float("inf"), device=DEV)
+    before = stray.grad.clone()
+    with pytest.raises(RuntimeError, match="non-finite"):
+        mg.clip_grad_norm_([stray], 1.0, error_if_nonfinite=True)
+    torch.cuda.synchronize()
+    assert torch.equal(stray.grad, before)
+    params[0].grad[0, 0] = float("inf")
+    ref_params[0].grad[0, 0] = float("inf")
+    with pytest.raises(RuntimeError, match="non-finite"):
+        mg.clip_grad_norm_(params, 1.0, error_if_nonfinite=True)
+    opt.step()      # no clip pending: the same as an optimizer that never clipped
+    ref.step()
+    torch.cuda.synchronize()
+    for x, y in zip(params, ref_params):
+        assert torch.equal(x.detach().isnan(), y.detach().isnan())
+        assert torch.equal(torch.nan_to_num(x.detach()), torch.nan_to_num(y.detach()))
