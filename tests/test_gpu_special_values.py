@@ -132,3 +132,46 @@ def test_unscale_overflow_below_unit_scale_propagates_nan_like_torch():
             nan_tensors.append((i, np.flatnonzero(np.isnan(st["p"])).tolist()))
     assert nan_tensors == [(1, [17])], nan_tensors
     log(f"[unscale_overflow] NaN only at {nan_tensors}, as in torch")
+
+
+def test_zero_eps_with_zero_gradients_gives_nan_where_torch_does():
+    """eps = 0 and a zero gradient on fresh state: the first step divides
+    m = 0 by sqrt(v) / sqrt(bc2) + eps = 0 (adam.py:537-547), so torch's CPU
+    path writes NaN into exactly those parameter elements; the GPU does the
+    same, and every other element agrees with the oracle bit for bit and with
+    torch within the state tolerance."""
+    from oracle.torch_path import TorchReferencePath
+
+    inject = {1: [(0, 5, 0.0), (1, 4098, 0.0), (4, 0, 0.0)]}
+    log("case: eps 0 with zero gradients at step 1")
+    pair = Pair(Case(shapes=SHAPES, steps=3, sigma=1e-3, eps=0.0, max_norm=None, chunk_elems=1024, inject=inject))
+    init = [p.detach().cpu().numpy().copy() for p in pair.params]
+    hp = [dict(betas=pair.case.betas, eps=0.0, weight_decay=pair.case.wd), dict(betas=pair.case.betas, eps=0.0,
+                                                                                 weight_decay=0.0)]
+    ref = TorchReferencePath(init, pair.group_of, hp, scaler=None, max_norm=None)
+    zeros_at_step1 = None
+    for s in range(1, 4):
+        lr = mg.cosine_lr(s - 1, *pair.case.lr_sched)
+        mg.set_optimizer_lr(pair.opt, lr)
+        pair.fill_grads(s)
+        if s == 1:   # the injected zeros, plus any the generator itself produced
+            zeros_at_step1 = [(i, np.flatnonzero(g.detach().cpu().numpy().ravel() == 0.0).tolist())
+                              for i, g in enumerate(pair.current_grads())]
+            zeros_at_step1 = [z for z in zeros_at_step1 if z[1]]
+        pair.oracle_step(s, lr)
+        ref.step([g.detach().cpu().numpy() for g in pair.current_grads()], lr)
+        pair.gpu_step()
+    torch.cuda.synchronize()
+    nan_at = []
+    for i in range(len(pair.params)):
+        st = pair.gpu_state(i)
+        tp, tm, tv, _ = ref.state(i)
+        for k, orc, tor in (("p", pair.orc.p[i], tp), ("m", pair.orc.m[i], tm), ("v", pair.orc.v[i], tv)):
+            ok, r = _same_with_nans(st[k], orc.ravel())
+            assert ok and r == 0.0, ("oracle", k, i, r)
+            ok, r = _same_with_nans(st[k], tor.ravel())
+            assert ok and r <= RTOL_STATE, ("torch", k, i, r)
+        if np.isnan(st["p"]).any():
+            nan_at.append((i, np.flatnonzero(np.isnan(st["p"])).tolist()))
+    assert nan_at == zeros_at_step1, (nan_at, zeros_at_step1)
+    assert {(0, 5), (1, 4098), (4, 0)} <= {(i, k) for i, ks in nan_at for k in ks}
