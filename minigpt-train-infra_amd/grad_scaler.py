@@ -187,6 +187,12 @@ class GradScaler:
     def _get_scale_async(self) -> torch.Tensor | None:
         return self._scale
 
+    def _found_inf_per_device(self, optimizer) -> dict:
+        """{device: found_inf} recorded by unscale_ for this optimizer
+        (grad_scaler.py:465-467): a device tensor that the coming norm pass
+        fills, 1.0 when a scaled gradient is inf or NaN."""
+        return self._per_optimizer_states[id(optimizer)]["found_inf_per_device"]
+
     def get_scale(self) -> float:
         if self._enabled:
             return self._init_scale if self._scale is None else float(self._scale.item())

@@ -420,10 +420,13 @@ def test_scaler_stage_errors_match_torch():
         sc.unscale_(opt)  # scale() never called
     sc.scale(torch.ones((), device=DEV))
     _grads(params, 1, 1.0)
+    params[0].grad[2] = float("nan")
     sc.unscale_(opt)
     with pytest.raises(RuntimeError, match="already been called"):
         sc.unscale_(opt)
     sc.step(opt)
+    (dev, found), = sc._found_inf_per_device(opt).items()   # filled on the GPU by the norm pass
+    assert dev == torch.device(DEV) and float(found) == 1.0
     with pytest.raises(RuntimeError, match="after step"):
         sc.unscale_(opt)
     with pytest.raises(RuntimeError, match="already been called since the last update"):
