@@ -87,18 +87,19 @@ typedef struct mgopt_group_hparams {
 
 typedef struct mgopt_plan mgopt_plan;
 
-/* Builds the device chunk table for a parameter set (the multi-tensor
+/* Builds the device chunk tables for a parameter set (the multi-tensor
  * dispatch torch builds per call in torch/optim/adam.py:139-212 _init_group
- * and in _foreach_norm's tensor lists, clip_grad.py:85-96).  steps_dev is a
+ * and in _foreach_norm's tensor lists, clip_grad.py:85-96): pass 2 (the AdamW
+ * update) works in chunks of chunk_elems elements, which must be a positive
+ * multiple of 512; pass 1 (the norm) in chunks of 65,536.  steps_dev is a
  * caller-owned float[n_tensors] holding each tensor's AdamW step count
- * (torch/optim/adam.py:168-176 state["step"]).  chunk_elems must be a positive
- * multiple of 512. */
+ * (torch/optim/adam.py:168-176 state["step"]). */
 MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensors, int32_t n_groups,
                                 float* steps_dev, int64_t chunk_elems, mgopt_plan** out);
 
 MGOPT_API int mgopt_plan_destroy(mgopt_plan* plan);
 
-/* Number of chunks (work-groups per pass) of the plan. */
+/* Number of pass-2 chunks of the plan (one work-group each). */
 MGOPT_API int64_t mgopt_plan_num_chunks(const mgopt_plan* plan);
 
 /* Sets the gradient of every tensor for the coming step from a host array of
