@@ -32,8 +32,20 @@
  *     sequentially, whose relative error grows with tensor size (about 3e-5
  *     at 2M elements, 2e-3 at 38.6M).
  *
- * Build: oracle/Makefile (gcc -O2 -ffp-contract=off so that every fused
- * multiply-add below is explicit).
+ * Pinning.  Every restated function is checked by tests that a plausible
+ * mistake fails, so none is "parity unpinned":
+ *   - against torch 2.10.0 CPU golden vectors (tests/golden/, written by
+ *     tests/golden/make_golden.py) and torch's CPU path run live on 40 seeded
+ *     configurations (tests/test_oracle_random.py);
+ *   - against closed forms (first step, zero gradient, bias corrections, exact
+ *     rational norms, cosine schedule values, the scaler trajectory);
+ *   - with six planted mistakes in the AdamW restatement, each rejected
+ *     (tests/test_oracle_pinning.py).
+ * orc_synth_value is the test-data generator, not reference arithmetic: it is
+ * pinned against the GPU generator bit for bit (tests/test_gpu_parity.py).
+ *
+ * Build: oracle/Makefile (gcc -O3 -mfma -ffp-contract=off: the compiler forms
+ * no fused multiply-add of its own, so every one below is an explicit fmaf).
  */
 #include <math.h>
 #include <stdint.h>
