@@ -41,11 +41,11 @@ def _align(n: int) -> int:
     return (n + ALIGN_ELEMS - 1) // ALIGN_ELEMS * ALIGN_ELEMS
 
 
-def bias_correction_table(beta1: float, beta2: float, cap: int) -> list[float]:
-    """[bc1(t), sqrt(bc2)(t)] for t in 0..cap-1, formed exactly as
+def bias_correction_table(beta1: float, beta2: float, cap: int, start: int = 0) -> list[float]:
+    """[bc1(t), sqrt(bc2)(t)] for t in start..cap-1, formed exactly as
     torch/optim/adam.py:529-536 forms them from step = state["step"].item()."""
     out: list[float] = []
-    for t in range(cap):
+    for t in range(start, cap):
         step = float(t)
         bias_correction1 = 1 - beta1**step
         bias_correction2 = 1 - beta2**step
@@ -146,6 +146,7 @@ class _Engine:
         self.t_bound = 0                     # upper bound of any step count reachable next step
         self.bc_cap = 0
         self.bc_keys: list[tuple[float, float]] = []
+        self.bc_host: list[list[float]] = []     # host copy of each group's table row
         self.bc_src: list[tuple] | None = None   # the hp_key the table was last checked against
         self.bc_table: torch.Tensor | None = None
         self.hp = None                       # GroupHparams array passed to mgopt_adamw_step
@@ -343,11 +344,17 @@ class _Engine:
         cap = max(BC_INITIAL_CAP, self.bc_cap)
         while cap < need:
             cap *= 2
-        flat: list[float] = []
+        # the host rows of groups whose betas are unchanged are extended, not
+        # recomputed: a doubling at step t costs t new entries, not 2t
+        old = dict(zip(self.bc_keys, self.bc_host)) if self.bc_table is not None else {}
+        rows = []
         for b1, b2 in keys:
-            flat.extend(bias_correction_table(b1, b2, cap))
-        table = torch.tensor(flat, dtype=torch.float64).to(self.device)
-        self.bc_table, self.bc_cap, self.bc_keys = table, cap, keys
+            row = old.get((b1, b2))
+            row = list(row) if row is not None else []
+            row.extend(bias_correction_table(b1, b2, cap, start=len(row) // 2))
+            rows.append(row)
+        table = torch.tensor([x for row in rows for x in row], dtype=torch.float64).to(self.device)
+        self.bc_table, self.bc_cap, self.bc_keys, self.bc_host = table, cap, keys, rows
 
     def sync_master(self) -> None:
         """Copies bf16/fp16 parameters into the fp32 master (exact widening)."""

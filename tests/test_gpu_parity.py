@@ -128,3 +128,25 @@ def test_ragged_tensor_list_scaler_dynamics():
     assert np.all(steps == 2000 - len(bad_steps))
     assert pair.opt._engine.error_flag() == 0
     log(f"[ragged] final scale {gpu_scales[-1]} tracker {tracker}")
+
+
+def test_past_the_first_bias_correction_table_doubling():
+    """1,100 steps (the bias-correction table starts at 1,024 steps and grows
+    by extending each group's row), with the no-decay group's betas changed at
+    step 600 (its row is rebuilt): all state bit-exact against the oracle."""
+    shapes = [("w", (48, 37)), ("b", (37,)), ("v", (513,))]
+    log("case: 1100 steps across the bias-correction table growth, betas change at 600")
+    pair = Pair(Case(shapes=shapes, steps=1, sigma=1e-2, max_norm=1.0))
+    for s in range(1, 1101):
+        if s == 600:
+            pair.opt.param_groups[1]["betas"] = (0.8, 0.99)
+            pair.orc.hparams[1]["betas"] = (0.8, 0.99)
+        lr = mg.cosine_lr(s - 1, 3e-4, 3e-5, 10, 1100)
+        mg.set_optimizer_lr(pair.opt, lr)
+        pair.fill_grads(s)
+        pair.oracle_step(s, lr)
+        pair.gpu_step()
+    torch.cuda.synchronize()
+    assert pair.opt._engine.bc_cap == 2048
+    check_pair(pair, label="table_growth")
+    assert all(float(pair.opt.state[p]["step"]) == 1100.0 for p in pair.params)

@@ -92,6 +92,8 @@ def test_bias_correction_table_matches_oracle():
         tab = eng.bias_correction_table(b1, b2, 300)
         for t in (1, 2, 3, 17, 100, 299):
             assert (tab[2 * t], tab[2 * t + 1]) == O.bias_corrections(b1, b2, float(t))
+        # a row extended from 100 to 300 steps equals the row computed whole
+        assert eng.bias_correction_table(b1, b2, 100) + eng.bias_correction_table(b1, b2, 300, start=100) == tab
 
 
 def test_library_exports_every_declared_symbol():
