@@ -20,6 +20,7 @@ import importlib
 import json
 import math
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -30,7 +31,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 importlib.import_module("__graft_entry__").ensure_built()   # builds only on a fresh checkout
-mg = importlib.import_module("minigpt-train-infra_amd")
+PKG_DIR = "minigpt-train-infra_amd"
+mg = importlib.import_module(PKG_DIR)
 syn = importlib.import_module("minigpt-train-infra_amd.synthetic")
 
 METRIC = "optimizer steps/sec + achieved HBM GB/s (% of peak) at Qwen3-8B-shaped 8.2B params"
@@ -213,6 +215,10 @@ def main() -> int:
     ap.add_argument("--vs-torch", action="store_true",
                     help="instead of the benchmark line, time torch's own GPU path (the reference's fused AdamW + "
                          "GradScaler + clip_grad_norm_) beside this package on fp32 params and grads of the workload")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="instead of the benchmark line, run the streaming-bandwidth probe (kernels with pass 2's "
+                         "launch shape: read, write, copy, three streams in place, pass 2's byte mix) and print "
+                         "its JSON lines")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB fp32 device copy (reads 1 GiB, writes 1 GiB) three times, "
                          "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -221,6 +227,12 @@ def main() -> int:
         print("bench.py measures one GPU only: the optimizer step here has no multi-GPU path (use --gpus 1)", file=sys.stderr)
         return 2
 
+    if args.stream_probe:
+        # a child process (it initialises the GPU itself); this process has not touched the GPU
+        probe = ROOT / PKG_DIR / "_build" / "stream_probe"
+        if not probe.exists():
+            importlib.import_module(f"{PKG_DIR}.build").build_probe()
+        return subprocess.run([str(probe)], check=False).returncode
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.calibrate_copy:
