@@ -167,11 +167,14 @@ class _Engine:
             N.load_library().mgopt_plan_destroy(ctypes.c_void_p(self.plan))
             self.plan = None
 
-    def __del__(self):
-        # (no imports here: at interpreter shutdown the import system is gone)
-        if sys.is_finalizing():
-            return  # the HIP runtime may already be gone; the process releases everything
+    def __del__(self, _finalizing=sys.is_finalizing):
+        # At interpreter shutdown module globals (sys, the library handle) may
+        # already be None, so the check is bound when the class is defined;
+        # then the HIP runtime may be gone too and the process releases
+        # everything itself.
         try:
+            if _finalizing():
+                return
             self.close()
         except Exception:
             pass

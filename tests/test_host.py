@@ -223,3 +223,14 @@ def test_step_is_wrapped_once_with_torch_hook_semantics(mg):
     mg.AdamW([nn.Parameter(torch.zeros(3))], lr=1e-3)
     assert mg.AdamW.step.__wrapped__ is raw
     assert not hasattr(raw, "__wrapped__")
+
+
+def test_engine_finalizer_survives_module_teardown(monkeypatch):
+    """At interpreter shutdown module globals are set to None before the last
+    objects are collected; the engine's finalizer must not depend on them."""
+    eng = importlib.import_module("minigpt-train-infra_amd.engine")
+    e = eng._Engine.__new__(eng._Engine)
+    e.plan = None
+    monkeypatch.setattr(eng, "sys", None)
+    monkeypatch.setattr(eng, "N", None)
+    e.__del__()   # no exception
