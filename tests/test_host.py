@@ -234,3 +234,15 @@ def test_engine_finalizer_survives_module_teardown(monkeypatch):
     monkeypatch.setattr(eng, "sys", None)
     monkeypatch.setattr(eng, "N", None)
     e.__del__()   # no exception
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N with N > 1 exits with a message
+    before touching any GPU."""
+    import subprocess
+    import sys as _sys
+
+    r = subprocess.run([_sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=300, cwd=str(ROOT))
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
