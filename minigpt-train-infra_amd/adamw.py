@@ -18,6 +18,7 @@ Differences a caller can observe, all by design:
 
 from __future__ import annotations
 
+import copy
 import functools
 import weakref
 from collections import defaultdict
@@ -273,15 +274,20 @@ class AdamW(torch.optim.Optimizer):
             torch._foreach_copy_(dst, src)
         self._installed.update(i for i, _ in items)
 
-    def _sync_all_masters(self) -> None:
-        """Master copies start from the current bf16/fp16 parameters; saved
-        masters copied in afterwards take precedence."""
+    def _sync_all_masters(self, keep: frozenset[int] | set[int] = frozenset()) -> None:
+        """Master copies start from the current bf16/fp16 parameters (one
+        multi-tensor copy, exact widening); the masters of the tensors in
+        `keep` are left alone because a loaded state supplies them."""
         eng = self._get_engine()
         if not eng.has_master or eng.master_synced:
             return
+        dst, src = [], []
         for i, p in enumerate(eng.params):
-            if "master_param" in eng.views[i]:
-                eng.views[i]["master_param"].copy_(p.detach())
+            if "master_param" in eng.views[i] and i not in keep:
+                dst.append(eng.views[i]["master_param"])
+                src.append(p.detach())
+        if dst:
+            torch._foreach_copy_(dst, src)
         eng.master_synced = True
 
     def _install_views(self, only_existing: bool = False) -> None:
@@ -426,8 +432,16 @@ class AdamW(torch.optim.Optimizer):
 
     @torch.no_grad()
     def load_state_dict(self, state_dict: dict[str, Any]) -> None:
+        # torch's order (torch/optim/optimizer.py:877-1017): a shallow copy that
+        # the load-state-dict pre hooks may replace, saved groups deep-copied,
+        # post hooks after the load
+        state_dict = state_dict.copy()
+        for pre_hook in self._optimizer_load_state_dict_pre_hooks.values():
+            hook_result = pre_hook(self, state_dict)
+            if hook_result is not None:
+                state_dict = hook_result
         groups = self.param_groups
-        saved_groups = state_dict["param_groups"]
+        saved_groups = copy.deepcopy(state_dict["param_groups"])
         if len(groups) != len(saved_groups):
             raise ValueError("loaded state dict has a different number of parameter groups")
         if any(len(g["params"]) != len(s["params"]) for g, s in zip(groups, saved_groups)):
@@ -446,24 +460,30 @@ class AdamW(torch.optim.Optimizer):
                 ng["param_names"] = g["param_names"]
             new_groups.append(ng)
         self.param_groups = new_groups
-        # loading replaces all state: parameters absent from the saved state
-        # start fresh (their moment segments are zeroed; the others are
-        # overwritten by the copy)
+        # Loading replaces all state: parameters absent from the saved state
+        # start fresh.  Nothing a present entry supplies is cleared or
+        # re-synced first: the entries may be views of these very arenas (a
+        # state_dict() of this optimizer, loaded back), as torch's
+        # state_dict() hands out its live tensors.
         items = [(index[id(id_to_param[pid])], entry) for pid, entry in state_dict["state"].items() if pid in id_to_param]
         present = {i for i, _ in items}
-        fresh = [eng.views[i][k] for i in range(len(eng.params)) if i not in present for k in ("exp_avg", "exp_avg_sq")]
+        absent = [i for i in range(len(eng.params)) if i not in present]
+        fresh = [eng.views[i][k] for i in absent for k in ("exp_avg", "exp_avg_sq")]
         if fresh:
             torch._foreach_zero_(fresh)
-        eng.steps.zero_()
+        if absent:
+            eng.steps[torch.tensor(absent, device=eng.device)] = 0.0
         self._installed.clear()
         eng.master_synced = False
-        self._sync_all_masters()
+        self._sync_all_masters(keep={i for i, e in items if e.get("master_param") is not None})
         self._copy_in_many(items)
         dict.clear(self.state)
         self._install_views(only_existing=True)
         eng.t_bound = int(eng.steps.max().item())
         eng.reset_iteration()
         self._state_dirty = False
+        for post_hook in self._optimizer_load_state_dict_post_hooks.values():
+            post_hook(self)
 
     def __setstate__(self, state: dict[str, Any]) -> None:
         super().__setstate__(state)

@@ -768,3 +768,67 @@ def test_nonfinite_error_leaves_gradients_unclipped():
     for x, y in zip(params, ref_params):
         assert torch.equal(x.detach().isnan(), y.detach().isnan())
         assert torch.equal(torch.nan_to_num(x.detach()), torch.nan_to_num(y.detach()))
+
+
+def test_load_state_dict_hooks_run_as_in_torch():
+    """Load-state-dict pre hooks may replace the dict, post hooks run after
+    the load, and the saved param_groups are copied rather than shared
+    (torch/optim/optimizer.py:877-1017)."""
+    params = _params([(30, 4), (9,)])
+    opt = mg.AdamW(params, lr=1e-3)
+    opt.param_groups[0]["tags"] = ["base"]               # extra group keys are kept, as torch keeps them
+    _grads(params, 1, 0.1)
+    opt.step()
+    sd = opt.state_dict()
+    calls = []
+
+    def pre(o, d):
+        d = dict(d)
+        d["param_groups"] = [dict(g, lr=5e-4) for g in d["param_groups"]]
+        calls.append("pre")
+        return d
+
+    h1 = opt.register_load_state_dict_pre_hook(pre)
+    h2 = opt.register_load_state_dict_post_hook(lambda o: calls.append(("post", o.param_groups[0]["lr"])))
+    opt.load_state_dict(sd)
+    h1.remove()
+    h2.remove()
+    assert calls == ["pre", ("post", 5e-4)]
+    assert sd["param_groups"][0]["lr"] == 1e-3          # the caller's dict is untouched
+    opt.param_groups[0]["tags"].append("loaded")
+    assert sd["param_groups"][0]["tags"] == ["base"]     # groups were deep-copied on load
+    _grads(params, 2, 0.1)
+    opt.step()
+    torch.cuda.synchronize()
+    assert float(opt.state[params[0]]["step"]) == 2.0
+
+
+def test_loading_this_optimizers_own_state_dict_changes_nothing():
+    """state_dict() hands out live views of the arenas (torch hands out its
+    live tensors); loading that dict back must leave every step count,
+    moment and fp32 master bit for bit as it was, and the run continues as an
+    optimizer that never reloaded."""
+    shapes = [(40, 24), (24,), (300,)]
+    pa, pb = _params(shapes, torch.bfloat16), _params(shapes, torch.bfloat16)
+    oa, ob = mg.AdamW(pa, lr=1e-3), mg.AdamW(pb, lr=1e-3)
+    for s in range(1, 4):
+        _grads(pa, s, 0.05)
+        _grads(pb, s, 0.05)
+        oa.step()
+        ob.step()
+    before = [{k: v.clone() for k, v in oa.state[p].items()} for p in pa]
+    oa.load_state_dict(oa.state_dict())
+    torch.cuda.synchronize()
+    for p, snap in zip(pa, before):
+        for k, v in snap.items():
+            assert torch.equal(oa.state[p][k], v), k
+    for s in range(4, 6):
+        _grads(pa, s, 0.05)
+        _grads(pb, s, 0.05)
+        oa.step()
+        ob.step()
+    torch.cuda.synchronize()
+    for x, y in zip(pa, pb):
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+        for k in ("step", "exp_avg", "exp_avg_sq", "master_param"):
+            assert torch.equal(oa.state[x][k], ob.state[y][k]), k
