@@ -485,6 +485,29 @@ class AdamW(torch.optim.Optimizer):
         for post_hook in self._optimizer_load_state_dict_post_hooks.values():
             post_hook(self)
 
+    def __getstate__(self) -> dict[str, Any]:
+        # torch pickles defaults, state and param_groups
+        # (torch/optim/optimizer.py:415-420); this optimizer's own settings
+        # travel with them, the device engine does not
+        st = super().__getstate__()
+        st["state"] = dict(self.state)
+        st.update(_master_weights=self._master_weights, _writeback=self._writeback, _chunk_elems=self._chunk_elems)
+        return st
+
     def __setstate__(self, state: dict[str, Any]) -> None:
         super().__setstate__(state)
+        self.__dict__.setdefault("_master_weights", None)
+        self.__dict__.setdefault("_writeback", False)
+        self.__dict__.setdefault("_chunk_elems", None)
         self._engine = None
+        self._installed = set()
+        tracked = _TrackedState(self)
+        dict.update(tracked, self.state)
+        self.state = tracked
+        # the unpickled state tensors are copied into a new engine's arenas
+        # at the first step, as directly assigned state is
+        self._state_dirty = bool(tracked)
+        me = weakref.ref(self)
+        for group in self.param_groups:
+            for p in group["params"]:
+                _OWNER[p] = me

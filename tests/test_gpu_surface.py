@@ -832,3 +832,28 @@ def test_loading_this_optimizers_own_state_dict_changes_nothing():
         assert torch.equal(x.view(torch.int16), y.view(torch.int16))
         for k in ("step", "exp_avg", "exp_avg_sq", "master_param"):
             assert torch.equal(oa.state[x][k], ob.state[y][k]), k
+
+
+def test_pickled_optimizer_continues_bit_exact():
+    """An AdamW pickled after three steps (its parameters and state travel
+    with it) continues exactly as the original does: the unpickled state,
+    fp32 masters included, is copied into the new engine at the first step."""
+    import pickle
+
+    params = _params([(33, 20), (20,)], torch.bfloat16)
+    opt = mg.AdamW([{"params": params[:1], "weight_decay": 0.1}, {"params": params[1:], "weight_decay": 0.0}], lr=1e-3)
+    for s in range(1, 4):
+        _grads(params, s, 0.05)
+        opt.step()
+    twin = pickle.loads(pickle.dumps(opt))
+    tparams = [p for g in twin.param_groups for p in g["params"]]
+    for s in range(4, 7):
+        _grads(params, s, 0.05)
+        _grads(tparams, s, 0.05)
+        opt.step()
+        twin.step()
+    torch.cuda.synchronize()
+    for x, y in zip(params, tparams):
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+        for k in ("step", "exp_avg", "exp_avg_sq", "master_param"):
+            assert torch.equal(opt.state[x][k], twin.state[y][k]), k

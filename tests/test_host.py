@@ -246,3 +246,25 @@ def test_bench_refuses_more_than_one_gpu():
                        timeout=300, cwd=str(ROOT))
     assert r.returncode == 2
     assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_pickled_optimizer_keeps_its_settings(mg):
+    """torch pickles only defaults, state and param_groups; the settings of
+    this AdamW travel too, the unpickled parameters are registered for the
+    fused clip, and the first step asks for a GPU rather than failing on a
+    missing attribute."""
+    import pickle
+
+    p = nn.Parameter(torch.zeros(6))
+    opt = mg.AdamW([p], lr=2e-3, chunk_elems=2048, writeback_grads=True)
+    opt.state[p] = {"step": torch.tensor(3.0), "exp_avg": torch.ones(6), "exp_avg_sq": torch.ones(6)}
+    o2 = pickle.loads(pickle.dumps(opt))
+    assert (o2._chunk_elems, o2._writeback, o2._master_weights) == (2048, True, None)
+    q = o2.param_groups[0]["params"][0]
+    assert float(o2.state[q]["step"]) == 3.0 and o2._state_dirty
+    adamw = importlib.import_module("minigpt-train-infra_amd.adamw")
+    assert adamw._OWNER.get(q)() is o2
+    q.grad = torch.ones(6)
+    if not torch.cuda.is_available():
+        with pytest.raises(RuntimeError):
+            o2.step()
