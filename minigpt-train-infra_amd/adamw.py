@@ -309,6 +309,11 @@ class AdamW(torch.optim.Optimizer):
             with torch.enable_grad():
                 loss = closure()
         eng = self._get_engine()
+        if torch.cuda.is_current_stream_capturing():
+            # as torch's non-capturable optimizers refuse (optimizer.py:451-478):
+            # a replay would reuse this step's learning rate and host-side state
+            raise RuntimeError("Attempting graph capture of step() for an instance of this AdamW, which runs with "
+                               "capturable=False: the learning rate and step bookkeeping are host-side")
         if self._state_dirty:
             with torch.no_grad():
                 self._reconcile_state()

@@ -857,3 +857,23 @@ def test_pickled_optimizer_continues_bit_exact():
         assert torch.equal(x.view(torch.int16), y.view(torch.int16))
         for k in ("step", "exp_avg", "exp_avg_sq", "master_param"):
             assert torch.equal(opt.state[x][k], twin.state[y][k]), k
+
+
+def test_step_refuses_graph_capture(monkeypatch):
+    """Like torch's optimizers built with capturable=False, step() raises when
+    the current stream is capturing a graph (the query is patched here: no
+    capture is started on the GPU), and nothing is launched."""
+    params = _params([(16, 4)])
+    opt = mg.AdamW(params, lr=1e-3)
+    _grads(params, 1, 0.1)
+    opt.step()
+    torch.cuda.synchronize()
+    before = params[0].detach().clone()
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    _grads(params, 2, 0.1)
+    with pytest.raises(RuntimeError, match="graph capture"):
+        opt.step()
+    monkeypatch.undo()
+    torch.cuda.synchronize()
+    assert torch.equal(params[0].detach(), before)
+    assert float(opt.state[params[0]]["step"]) == 1.0
