@@ -91,7 +91,7 @@ typedef struct mgopt_plan mgopt_plan;
  * dispatch torch builds per call in torch/optim/adam.py:139-212 _init_group
  * and in _foreach_norm's tensor lists, clip_grad.py:85-96): pass 2 (the AdamW
  * update) works in chunks of chunk_elems elements, which must be a positive
- * multiple of 512; pass 1 (the norm) in chunks of 65,536.  steps_dev is a
+ * multiple of 512; pass 1 (the norm) in chunks of 131,072.  steps_dev is a
  * caller-owned float[n_tensors] holding each tensor's AdamW step count
  * (torch/optim/adam.py:168-176 state["step"]). */
 MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensors, int32_t n_groups,

@@ -54,10 +54,12 @@ constexpr int kNormUnroll = 2;       // pass-1 4-element accesses in flight per 
 constexpr bool kNtNormLoad = true;   // nontemporal gradient loads in pass 1
 // pass 1 has its own chunk table of kNormChunk elements per chunk and
 // work-group, whatever the pass-2 chunk size: the finalize kernel then reads
-// one partial per 64K elements.  (A grid-stride form with 1024-4096
-// work-groups per class measured 0.1-0.15 ms slower per step on the Qwen3-8B
-// set than 64K elements per work-group.)
-constexpr int64_t kNormChunk = 65536;
+// one partial per 128K elements.  Pass 1 + finalize measured in one process
+// on the Qwen3-8B set: 16K-element chunks 2.94 ms, 32K 2.50, 64K 2.35,
+// 128K 2.29, 256K 2.31, 512K 2.31; above 128K the smaller sets lose (GPT-2
+// small 0.049 ms at 128K, 0.100 at 512K).  A grid-stride form with
+// 1024-4096 work-groups per class was slower still.
+constexpr int64_t kNormChunk = 131072;
 // A dispatch packet carries its grid size in work-items as a 32-bit value, so
 // launches over more chunks than fit are issued in pieces, each piece given
 // its first chunk (and first partial slot) as arguments.  8,388,607
@@ -388,9 +390,9 @@ __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
 __global__ void __launch_bounds__(kFinalizeBlock)
     finalize_kernel(const Partial* partials, int64_t n, double max_norm, float* norm_out, float* coef_out,
                     float* found_inf_out, Window* win) {
-    // each thread sums partials tid, tid + 1024, ... in that order (45 us for
-    // the 125K partials of the Qwen3-8B set: one CU's memory parallelism;
-    // unrolling the loads 8-deep measured the same)
+    // each thread sums partials tid, tid + 1024, ... in that order (bounded
+    // by one CU's memory parallelism: 45 us for 125K partials, unrolled
+    // 8-deep the same; the Qwen3-8B set has 62,633 at 128K-element chunks)
     double s = 0.0;
     uint32_t f = 0;
     for (int64_t i = threadIdx.x; i < n; i += kFinalizeBlock) {

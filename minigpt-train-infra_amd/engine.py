@@ -31,7 +31,7 @@ import torch
 from . import _native as N
 
 ALIGN_ELEMS = 64                    # 256 B of fp32 per arena segment
-DEFAULT_CHUNK = 1024                # elements per pass-2 work-group (pass 1 has its own 64K-element chunks):
+DEFAULT_CHUNK = 1024                # elements per pass-2 work-group (pass 1 has its own 128K-element chunks):
                                     # 512 threads over 1024 elements retire fast and keep half the waves
                                     # of a CU streaming; 2-13 % faster than 16384 from 124M to 8.2B params
 BC_INITIAL_CAP = 1024               # first bias-correction table size (steps)
