@@ -23,7 +23,7 @@ import ctypes
 import math
 import sys
 import weakref
-from typing import Any, Sequence
+from typing import Sequence
 
 import numpy as np
 import torch
