@@ -877,3 +877,33 @@ def test_step_refuses_graph_capture(monkeypatch):
     torch.cuda.synchronize()
     assert torch.equal(params[0].detach(), before)
     assert float(opt.state[params[0]]["step"]) == 1.0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_model_copy_rounding_at_the_edges(dtype):
+    """The bf16/fp16 model copy written from the fp32 master, at the edges of
+    the conversion: ties to even, overflow to inf, values just below it,
+    subnormals, signed zeros, infinities, NaN.  Masters are installed through
+    load_state_dict and a step with lr 0 and zero gradients leaves them as
+    they are, so the kernel's copy must equal torch's own conversion of them
+    (bit for bit; NaN as NaN: torch's CPU vector path writes bf16 NaN as
+    0xFFFF, its scalar and GPU paths as 0x7FC0, which this kernel writes)."""
+    vals = torch.tensor([0.0, -0.0, 1.0, 1.00390625, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -9, 3.3895314e38, 3.4028235e38,
+                         -3.4028235e38, 1e-40, -1e-40, 1e-45, 5.9604645e-08, 2.9802322e-08, 65504.0, 65520.0,
+                         65519.99, 1e5, float("nan"), float("inf"), float("-inf"), 6.1035156e-05, 6.0975552e-05],
+                        dtype=torch.float32)
+    n = vals.numel()
+    p = torch.nn.Parameter(torch.zeros(n, dtype=dtype, device=DEV))
+    opt = mg.AdamW([p], lr=0.0, weight_decay=0.0)
+    opt.load_state_dict({"state": {0: {"step": torch.tensor(0.0), "exp_avg": torch.zeros(n),
+                                       "exp_avg_sq": torch.zeros(n), "master_param": vals.clone()}},
+                         "param_groups": opt.state_dict()["param_groups"]})
+    p.grad = torch.zeros(n, dtype=dtype, device=DEV)
+    opt.step()
+    torch.cuda.synchronize()
+    got = p.detach().cpu()
+    want = vals.to(dtype)
+    nan = torch.isnan(vals)
+    assert torch.equal(torch.isnan(got.float()), nan)
+    assert torch.equal(got.view(torch.int16)[~nan], want.view(torch.int16)[~nan])
+    assert torch.equal(opt.state[p]["master_param"].cpu().view(torch.int32)[~nan], vals.view(torch.int32)[~nan])
