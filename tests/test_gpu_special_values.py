@@ -85,10 +85,16 @@ def test_norm_overflow_with_finite_gradients():
 
 
 def _same_with_nans(a: np.ndarray, b: np.ndarray) -> tuple[bool, float]:
+    """NaN in the same places, then the largest relative difference of the
+    other elements (equal values, infinities included, count as equal)."""
     na, nb = np.isnan(a), np.isnan(b)
     if not np.array_equal(na, nb):
         return False, math.inf
-    keep = ~na
+    keep = ~na & (a != b)
+    if not keep.any():
+        return True, 0.0
+    if np.isinf(a[keep]).any() or np.isinf(b[keep]).any():
+        return False, math.inf
     return True, maxrel(a[keep], b[keep])
 
 
@@ -175,3 +181,39 @@ def test_zero_eps_with_zero_gradients_gives_nan_where_torch_does():
             nan_at.append((i, np.flatnonzero(np.isnan(st["p"])).tolist()))
     assert nan_at == zeros_at_step1, (nan_at, zeros_at_step1)
     assert {(0, 5), (1, 4098), (4, 0)} <= {(i, k) for i, ks in nan_at for k in ks}
+
+
+def test_extreme_gradient_magnitudes_without_clipping():
+    """fp32 gradients whose squares overflow (1e20, 3e38) or underflow (1e-30)
+    the fp32 range, no scaler and no clip: v becomes inf (the update divides
+    by inf) or stays 0 (the denominator is eps); every element agrees with the
+    oracle bit for bit (NaN as NaN) and with torch's CPU path within the
+    state tolerance."""
+    from oracle.torch_path import TorchReferencePath
+
+    inject = {1: [(0, 3, 1e20), (1, 10, 3e38), (2, 7, -1e-30), (5, 100, 1e-30)],
+              2: [(0, 3, -1e20), (3, 2, 3e38)]}
+    log("case: extreme fp32 gradient magnitudes, no clip")
+    pair = Pair(Case(shapes=SHAPES, steps=3, sigma=1e-3, max_norm=None, chunk_elems=1024, inject=inject))
+    init = [p.detach().cpu().numpy().copy() for p in pair.params]
+    hp = [dict(betas=pair.case.betas, eps=pair.case.eps, weight_decay=pair.case.wd),
+          dict(betas=pair.case.betas, eps=pair.case.eps, weight_decay=0.0)]
+    ref = TorchReferencePath(init, pair.group_of, hp, scaler=None, max_norm=None)
+    for s in range(1, 4):
+        lr = mg.cosine_lr(s - 1, *pair.case.lr_sched)
+        mg.set_optimizer_lr(pair.opt, lr)
+        pair.fill_grads(s)
+        pair.oracle_step(s, lr)
+        ref.step([g.detach().cpu().numpy() for g in pair.current_grads()], lr)
+        pair.gpu_step()
+    torch.cuda.synchronize()
+    for i in range(len(pair.params)):
+        st = pair.gpu_state(i)
+        tp, tm, tv, _ = ref.state(i)
+        for k, orc, tor in (("p", pair.orc.p[i], tp), ("m", pair.orc.m[i], tm), ("v", pair.orc.v[i], tv)):
+            ok, r = _same_with_nans(st[k], orc.ravel())
+            assert ok and r == 0.0, ("oracle", k, i, r)
+            ok, r = _same_with_nans(st[k], tor.ravel())
+            assert ok and r <= RTOL_STATE, ("torch", k, i, r)
+    # the overflowed square keeps v at inf (beta2 * inf); the underflowed one left v finite
+    assert np.isinf(pair.gpu_state(1)["v"][10]) and np.isfinite(pair.gpu_state(5)["v"][100])
