@@ -797,12 +797,14 @@ int hip_fail(hipError_t e, const char* what) {
 // Runs the body with the plan's device current, restoring the caller's.
 struct DeviceGuard {
     int prev = -1;
-    bool ok = false;
+    bool switched = false;
     explicit DeviceGuard(int dev) {
-        if (hipGetDevice(&prev) == hipSuccess) ok = (prev == dev) || hipSetDevice(dev) == hipSuccess;
+        // restores the caller's device only when it had to switch: the common
+        // case (the plan's device is current) costs one hipGetDevice
+        if (hipGetDevice(&prev) == hipSuccess && prev != dev) switched = hipSetDevice(dev) == hipSuccess;
     }
     ~DeviceGuard() {
-        if (prev >= 0) (void)hipSetDevice(prev);
+        if (switched) (void)hipSetDevice(prev);
     }
 };
 
