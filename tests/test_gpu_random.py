@@ -9,11 +9,14 @@ Bar: skip decisions, scale, growth tracker and step counts bit-exact; fp32
 state (params or masters, exp_avg, exp_avg_sq) bit-exact; the bf16 / fp16
 model copy equal to the round-to-nearest-even image of the master; norms
 within 1e-5 relative.
+
+MGOPT_RANDOM_CASES=N runs seeds 0..N-1 instead of the default 24.
 """
 
 from __future__ import annotations
 
 import math
+import os
 
 import numpy as np
 import pytest
@@ -56,7 +59,7 @@ def _config(seed: int) -> dict:
                 lr=float(10.0 ** r.uniform(-4, -2)))
 
 
-@pytest.mark.parametrize("seed", list(range(24)))
+@pytest.mark.parametrize("seed", list(range(int(os.environ.get("MGOPT_RANDOM_CASES", "24")))))
 def test_random_configuration_against_the_oracle(seed):
     c = _config(seed)
     log(f"case: seed {seed} {c['pdt']}/{c['gdt']} sizes {c['sizes']} chunk {c['chunk']} scaler {bool(c['scaler'])} "
