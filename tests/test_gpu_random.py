@@ -1,9 +1,10 @@
 """GPU parity on 24 seeded random configurations against the oracle: parameter
 dtype (fp32, or bf16 / fp16 with an fp32 master), gradient dtype, tensor sizes
-(1 element to two chunks, odd sizes for the scalar tails), chunk size, one or
-two groups with random betas (both lerp branches), eps, weight decay and
-maximize, a GradScaler with a random initial scale and growth interval or
-none, clipping or none, and NaN / +inf / -inf injected on some steps.
+(1 element to several 131,072-element pass-1 chunks, odd sizes for the scalar
+tails), chunk size, one or two groups with random betas (both lerp branches),
+eps, weight decay and maximize, a GradScaler with a random initial scale and
+growth interval or none, clipping or none, and NaN / +inf / -inf injected at a
+random position on some steps.
 
 Bar: skip decisions, scale, growth tracker and step counts bit-exact; fp32
 state (params or masters, exp_avg, exp_avg_sq) bit-exact; the bf16 / fp16
@@ -42,7 +43,7 @@ def _config(seed: int) -> dict:
                            eps=float(10.0 ** r.uniform(-10, -3)), weight_decay=float(r.choice([0.0, 0.1, 0.3])),
                            maximize=bool(r.rand() < 0.2)))
     n_tensors = int(r.randint(2, 6))
-    sizes = [int(r.choice([1, 7, 64, 1001, 4096, 4099, 65536, 70001])) for _ in range(n_tensors)]
+    sizes = [int(r.choice([1, 7, 64, 1001, 4096, 4099, 65536, 70001, 131073, 300001])) for _ in range(n_tensors)]
     group_of = [k % n_groups for k in range(n_tensors)]
     scaler = None
     if r.rand() < 0.6:
@@ -56,14 +57,14 @@ def _config(seed: int) -> dict:
     return dict(pdt=pdt, gdt=gdt, groups=groups, sizes=sizes, group_of=group_of, scaler=scaler,
                 max_norm=None if r.rand() < 0.3 else float(r.choice([0.05, 1.0])), steps=steps, bad=bad,
                 chunk=int(r.choice([512, 1024, 4096, 65536])), sigma=float(10.0 ** r.uniform(-3, -1)),
-                lr=float(10.0 ** r.uniform(-4, -2)))
+                lr=float(10.0 ** r.uniform(-4, -2)), bad_pos=float(r.rand()))
 
 
 @pytest.mark.parametrize("seed", list(range(int(os.environ.get("MGOPT_RANDOM_CASES", "24")))))
 def test_random_configuration_against_the_oracle(seed):
     c = _config(seed)
     log(f"case: seed {seed} {c['pdt']}/{c['gdt']} sizes {c['sizes']} chunk {c['chunk']} scaler {bool(c['scaler'])} "
-        f"clip {c['max_norm']} bad {sorted(c['bad'])}")
+        f"clip {c['max_norm']} bad {sorted(c['bad'])} at {c['bad_pos']:.3f}")
     params = []
     for i, n in enumerate(c["sizes"]):
         p = torch.empty(n, dtype=DT[c["pdt"]], device=DEV)
@@ -91,7 +92,8 @@ def test_random_configuration_against_the_oracle(seed):
         for k, g in enumerate(grads):
             syn.fill_(g, 4, (s << 20) | (100 * seed + index[k]), c["sigma"] * scale)
         if s in c["bad"]:
-            grads[s % len(grads)].view(-1)[0] = c["bad"][s]
+            g = grads[s % len(grads)].view(-1)
+            g[int(c["bad_pos"] * g.numel())] = c["bad"][s]
         if not separate:
             for p, g in zip(order, grads):
                 p.grad = g
