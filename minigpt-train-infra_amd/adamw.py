@@ -85,14 +85,73 @@ def _call_with_hooks(func, self, args, kwargs):
     return out
 
 
+class _TrackedEntry(dict):
+    """One parameter's optimizer.state entry.  A write into it
+    (state[p]["step"] = ..., state[p]["exp_avg"] = ...) changes what torch's
+    next step reads; here it marks the optimizer so that the next step copies
+    the new value into the arenas."""
+
+    def __init__(self, owner: "weakref.ref[AdamW]", *args):
+        super().__init__(*args)
+        self._owner = owner
+
+    def _dirty(self) -> None:
+        opt = self._owner()
+        if opt is not None:
+            opt._state_dirty = True
+
+    def __setitem__(self, key, value):
+        super().__setitem__(key, value)
+        self._dirty()
+
+    def __delitem__(self, key):
+        super().__delitem__(key)
+        self._dirty()
+
+    def clear(self):
+        super().clear()
+        self._dirty()
+
+    def update(self, *args, **kwargs):
+        super().update(*args, **kwargs)
+        self._dirty()
+
+    def pop(self, *args):
+        r = super().pop(*args)
+        self._dirty()
+        return r
+
+    def popitem(self):
+        r = super().popitem()
+        self._dirty()
+        return r
+
+    def setdefault(self, key, default=None):
+        r = super().setdefault(key, default)
+        self._dirty()
+        return r
+
+    def __reduce__(self):
+        return (dict, (dict(self),))
+
+
 class _TrackedState(defaultdict):
-    """optimizer.state that notices when whole entries are replaced."""
+    """optimizer.state that notices when entries are replaced or written into."""
 
     def __init__(self, owner: "AdamW"):
-        super().__init__(dict)
+        super().__init__()
         # a weak reference: the optimizer owns this dict, and a cycle would keep
         # its device arenas alive until the cyclic collector runs
         self._owner = weakref.ref(owner)
+
+    def __missing__(self, key):
+        # torch's _init_group reads state[p] for a parameter without state
+        entry = _TrackedEntry(self._owner)
+        self[key] = entry
+        return entry
+
+    def entry(self, values: dict) -> _TrackedEntry:
+        return _TrackedEntry(self._owner, values)
 
     def _dirty(self) -> None:
         owner = self._owner()
@@ -117,6 +176,16 @@ class _TrackedState(defaultdict):
 
     def pop(self, *args):
         r = super().pop(*args)
+        self._dirty()
+        return r
+
+    def popitem(self):
+        r = super().popitem()
+        self._dirty()
+        return r
+
+    def setdefault(self, key, default=None):
+        r = super().setdefault(key, default)
         self._dirty()
         return r
 
@@ -220,7 +289,7 @@ class AdamW(torch.optim.Optimizer):
                     views["step"].zero_()
                     self._installed.discard(i)
                 continue
-            if all(entry.get(k) is views[k] for k in ("step", "exp_avg", "exp_avg_sq")):
+            if all(entry.get(k) is v for k, v in views.items()):
                 continue
             changed.append((i, entry))
         self._copy_in_many(changed)
@@ -295,7 +364,7 @@ class AdamW(torch.optim.Optimizer):
         for i, p in enumerate(eng.params):
             if only_existing and i not in self._installed:
                 continue
-            dict.__setitem__(self.state, p, dict(eng.views[i]))
+            dict.__setitem__(self.state, p, self.state.entry(eng.views[i]))
             self._installed.add(i)
 
     # ------------------------------------------------------------ surface
@@ -327,7 +396,7 @@ class AdamW(torch.optim.Optimizer):
         if grads is not None:
             for i, (p, g) in enumerate(zip(eng.params, grads)):
                 if g is not None and i not in self._installed:
-                    dict.__setitem__(self.state, p, dict(eng.views[i]))
+                    dict.__setitem__(self.state, p, self.state.entry(eng.views[i]))
                     self._installed.add(i)
         return loss
 
@@ -433,7 +502,11 @@ class AdamW(torch.optim.Optimizer):
         if self._state_dirty:
             with torch.no_grad():
                 self._reconcile_state()
-        return super().state_dict()
+        sd = super().state_dict()
+        # plain dicts, as torch's are: torch.load(weights_only=True) refuses
+        # any other class, and checkpoints are read that way
+        sd["state"] = {k: dict(v) for k, v in sd["state"].items()}
+        return sd
 
     @torch.no_grad()
     def load_state_dict(self, state_dict: dict[str, Any]) -> None:
@@ -495,7 +568,7 @@ class AdamW(torch.optim.Optimizer):
         # (torch/optim/optimizer.py:415-420); this optimizer's own settings
         # travel with them, the device engine does not
         st = super().__getstate__()
-        st["state"] = dict(self.state)
+        st["state"] = {k: dict(v) for k, v in self.state.items()}
         st.update(_master_weights=self._master_weights, _writeback=self._writeback, _chunk_elems=self._chunk_elems)
         return st
 

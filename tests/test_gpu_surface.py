@@ -293,6 +293,49 @@ def test_torch_adamw_state_dict_loads_and_continues():
                           "param_groups": opt.state_dict()["param_groups"]})
 
 
+def test_writes_into_state_entries_take_effect_as_in_torch():
+    """Writing into a parameter's state entry changes the next step exactly as
+    it does for torch's CPU AdamW: a step count reset to 0 and a zeroed
+    exp_avg on one tensor, a new exp_avg_sq on the other, after 3 steps; 3
+    more steps then match torch to 1e-6.  state_dict() entries are plain
+    dicts (torch.load(weights_only=True) accepts no other class)."""
+    shapes = [(40, 30), (30,)]
+    init = [O.synth(int(np.prod(s)), 1, 10 + i, O.synth_k(0.02)).reshape(s) for i, s in enumerate(shapes)]
+    cpu = [torch.nn.Parameter(torch.from_numpy(x.copy())) for x in init]
+    gpu = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in cpu]
+    kw = dict(lr=1e-3, betas=(0.9, 0.95), weight_decay=0.1)
+    topt = torch.optim.AdamW(cpu, fused=False, **kw)
+    opt = mg.AdamW(gpu, **kw)
+    gens = lambda s: [O.synth(int(np.prod(sh)), 2, (s << 20) | i, O.synth_k(1e-2)).reshape(sh) for i, sh in enumerate(shapes)]
+
+    def step(s):
+        for p, q, g in zip(cpu, gpu, gens(s)):
+            p.grad = torch.from_numpy(g)
+            q.grad = torch.from_numpy(g).to(DEV)
+        topt.step()
+        opt.step()
+
+    for s in range(1, 4):
+        step(s)
+    new_v = O.synth(30, 5, 7, O.synth_k(1e-3)).reshape(30) ** 2
+    topt.state[cpu[0]]["step"] = torch.tensor(0.0)
+    topt.state[cpu[0]]["exp_avg"] = torch.zeros(40, 30)
+    topt.state[cpu[1]]["exp_avg_sq"] = torch.from_numpy(new_v.copy())
+    opt.state[gpu[0]]["step"] = torch.tensor(0.0)
+    opt.state[gpu[0]]["exp_avg"] = torch.zeros(40, 30, device=DEV)
+    opt.state[gpu[1]]["exp_avg_sq"] = torch.from_numpy(new_v.copy()).to(DEV)
+    assert all(type(e) is dict for e in opt.state_dict()["state"].values())
+    for s in range(4, 7):
+        step(s)
+    torch.cuda.synchronize()
+    for p, q in zip(cpu, gpu):
+        assert float(opt.state[q]["step"]) == float(topt.state[p]["step"])
+        assert maxrel(q.detach().cpu().numpy(), p.detach().numpy()) <= RTOL_STATE
+        for k in ("exp_avg", "exp_avg_sq"):
+            assert maxrel(opt.state[q][k].cpu().numpy(), topt.state[p][k].numpy()) <= RTOL_STATE, k
+    assert float(opt.state[gpu[0]]["step"]) == 3.0 and float(opt.state[gpu[1]]["step"]) == 6.0
+
+
 def test_state_assigned_in_param_dtype_is_picked_up():
     """The reference's checkpoint-migration branch (src/minigpt/optim.py:242-251,
     124-133) clears optimizer.state and assigns every parameter a dict whose

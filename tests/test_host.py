@@ -268,3 +268,57 @@ def test_pickled_optimizer_keeps_its_settings(mg):
     if not torch.cuda.is_available():
         with pytest.raises(RuntimeError):
             o2.step()
+
+
+def test_writes_into_a_state_entry_mark_the_optimizer(mg):
+    """torch's state_dict() shares each parameter's state dict with
+    optimizer.state, so writing into either changes what torch's next step
+    reads.  Every way of writing into an entry marks this optimizer for a copy
+    into its arenas; reading does not; entries pickle and copy as plain dicts."""
+    import copy
+    import pickle
+
+    p = nn.Parameter(torch.zeros(4))
+    opt = mg.AdamW([p])
+    e = opt.state[p]                     # torch's _init_group creates the entry this way
+    assert isinstance(e, dict) and len(e) == 0
+    e["step"] = torch.tensor(0.0)
+    writes = [
+        lambda: e.__setitem__("step", torch.tensor(1.0)),
+        lambda: e.update(exp_avg=torch.zeros(4)),
+        lambda: e.setdefault("exp_avg_sq", torch.zeros(4)),
+        lambda: e.pop("exp_avg"),
+        lambda: e.__delitem__("exp_avg_sq"),
+        lambda: e.popitem(),
+        lambda: e.clear(),
+    ]
+    for w in writes:
+        opt._state_dirty = False
+        w()
+        assert opt._state_dirty
+    opt._state_dirty = False
+    e["step"] = torch.tensor(2.0)
+    opt._state_dirty = False
+    _ = (e.get("step"), dict(e), list(e.items()), opt.state.get(p))
+    assert not opt._state_dirty
+    for clone in (pickle.loads(pickle.dumps(e)), copy.deepcopy(e), copy.copy(e)):
+        assert type(clone) is dict and float(clone["step"]) == 2.0
+
+
+def test_state_dict_loads_with_weights_only(mg):
+    """state_dict() entries are plain dicts, so a checkpoint holding them
+    loads with torch.load(weights_only=True), which refuses other classes."""
+    import io
+
+    p = nn.Parameter(torch.zeros(3))
+    opt = mg.AdamW([p])
+    dict.__setitem__(opt.state, p, opt.state.entry({"step": torch.tensor(2.0), "exp_avg": torch.ones(3),
+                                                    "exp_avg_sq": torch.ones(3)}))
+    opt._state_dirty = False
+    sd = opt.state_dict()
+    assert all(type(e) is dict for e in sd["state"].values())
+    buf = io.BytesIO()
+    torch.save({"optimizer": sd}, buf)
+    buf.seek(0)
+    back = torch.load(buf, weights_only=True)
+    assert float(back["optimizer"]["state"][0]["step"]) == 2.0
