@@ -8,9 +8,10 @@ torch/optim/optimizer.py:677-767).
 
 Differences a caller can observe, all by design:
   - optimizer state lives in flat device arenas; optimizer.state[p] holds
-    views into them.  Assigning new tensors into optimizer.state (as
-    src/minigpt/optim.py:242-251 does when migrating checkpoints) is picked up
-    and copied into the arenas before the next step.
+    views into them.  Assigning new entries into optimizer.state (as
+    src/minigpt/optim.py:242-251 does when migrating checkpoints) or new
+    tensors into an entry is picked up and copied into the arenas before the
+    next step.  state_dict() entries are fresh dicts holding those views.
   - bf16/fp16 parameters are updated through an fp32 master copy (state key
     "master_param"); exp_avg/exp_avg_sq are always fp32.
   - amsgrad and differentiable are not supported (the reference uses neither).
