@@ -63,23 +63,40 @@ class TinyLM(nn.Module):
         return self.lm_head(self.ln_f(x))
 
 
-def _loop(model, opt, scaler, clip, batches, inf_step):
+def _loop(model, opt, scaler, clip, batches, inf_step, set_to_none=True, micro=1, scheduler=None):
+    """micro > 1: each batch is split into that many micro-batches whose
+    gradients accumulate (train.py:466-481); scheduler: a torch LR scheduler
+    stepped after each optimizer step instead of set_optimizer_lr."""
     losses, norms, scales = [], [], []
     for s, (x, y) in enumerate(batches, start=1):
-        mg.set_optimizer_lr(opt, mg.cosine_lr(s - 1, 3e-3, 3e-4, 5, len(batches)))
-        opt.zero_grad(set_to_none=True)
-        loss = nn.functional.cross_entropy(model(x).flatten(0, 1), y.flatten())
-        scaler.scale(loss).backward()
+        if scheduler is None:
+            mg.set_optimizer_lr(opt, mg.cosine_lr(s - 1, 3e-3, 3e-4, 5, len(batches)))
+        opt.zero_grad(set_to_none=set_to_none)
+        total = 0.0
+        for xm, ym in zip(x.chunk(micro), y.chunk(micro)):
+            loss = nn.functional.cross_entropy(model(xm).flatten(0, 1), ym.flatten()) / micro
+            scaler.scale(loss).backward()
+            total = total + loss.detach()
         if s == inf_step:
             model.blocks[1].fc.weight.grad.view(-1)[11] = float("inf")
         scaler.unscale_(opt)
         norms.append(clip(model.parameters(), 1.0))
         scaler.step(opt)
         scaler.update()
-        losses.append(loss.detach())
+        if scheduler is not None:
+            scheduler.step()
+        losses.append(total)
         scales.append(scaler.get_scale())
     torch.cuda.synchronize()
     return [float(v) for v in losses], [float(v) for v in norms], scales
+
+
+def _worst_param(ref_model, my_model):
+    worst = 0.0
+    for p, q in zip(ref_model.parameters(), my_model.parameters()):
+        d = (p.detach() - q.detach()).abs().max().item() / max(p.detach().abs().max().item(), 1e-30)
+        worst = max(worst, d)
+    return worst
 
 
 def test_training_loop_matches_torch_on_the_same_model():
@@ -108,10 +125,46 @@ def test_training_loop_matches_torch_on_the_same_model():
     finite = [(a, b) for a, b in zip(mine[1], ref[1]) if math.isfinite(b)]
     assert len(finite) == 39 and not math.isfinite(mine[1][12])
     worst_norm = max(abs(a - b) / abs(b) for a, b in finite)
-    worst_param = 0.0
-    for (n, p), q in zip(ref_model.named_parameters(), my_model.parameters()):
-        d = (p.detach() - q.detach()).abs().max().item() / max(p.detach().abs().max().item(), 1e-30)
-        worst_param = max(worst_param, d)
+    worst_param = _worst_param(ref_model, my_model)
     log(f"[train loop] worst rel: loss {worst_loss:.2e} norm {worst_norm:.2e} param {worst_param:.2e}")
+    assert worst_loss <= 1e-6 and worst_norm <= 1e-6 and worst_param <= 1e-5
+    assert my_opt._engine.error_flag() == 0
+
+
+def test_accumulation_in_place_zeroing_and_a_torch_scheduler():
+    """The same loop with gradients accumulated over 4 micro-batches,
+    zero_grad(set_to_none=False) (the .grad tensors persist and are zeroed in
+    place, so the optimizer sees the same gradient storage every step) and
+    torch's LambdaLR driving the learning rate; same bars as above."""
+    torch.manual_seed(2)
+    ref_model = TinyLM().to(DEV)
+    my_model = copy.deepcopy(ref_model)
+    g = torch.Generator(device="cpu").manual_seed(3)
+    batches = []
+    for _ in range(30):
+        x = torch.randint(0, 96, (8, 32), generator=g)
+        batches.append((x.to(DEV), torch.roll(x, -1, dims=1).to(DEV)))
+    kw = dict(lr=3e-3, betas=(0.9, 0.95), eps=1e-8)
+    ref_opt = torch.optim.AdamW(mg.build_adamw_param_groups(ref_model, 0.1), fused=False, foreach=False, **kw)
+    my_opt = mg.AdamW(mg.build_adamw_param_groups(my_model, 0.1), **kw)
+    decay = lambda s: 0.97 ** s
+    ref_sched = torch.optim.lr_scheduler.LambdaLR(ref_opt, decay)
+    my_sched = torch.optim.lr_scheduler.LambdaLR(my_opt, decay)
+    ref_scaler = torch.amp.GradScaler("cuda", init_scale=2.0**12, growth_interval=7)
+    my_scaler = mg.GradScaler("cuda", init_scale=2.0**12, growth_interval=7)
+
+    log("case: tiny LM, 4 micro-batches, zero_grad(set_to_none=False), LambdaLR, 30 steps, inf at step 9")
+    ref = _loop(ref_model, ref_opt, ref_scaler, torch.nn.utils.clip_grad_norm_, batches, 9, False, 4, ref_sched)
+    mine = _loop(my_model, my_opt, my_scaler, mg.clip_grad_norm_, batches, 9, False, 4, my_sched)
+
+    assert mine[2] == ref[2], (mine[2], ref[2])
+    assert mg.optimizer_completed_steps(my_opt) == mg.optimizer_completed_steps(ref_opt) == 29
+    assert my_opt.param_groups[0]["lr"] == ref_opt.param_groups[0]["lr"]
+    worst_loss = max(abs(a - b) / abs(b) for a, b in zip(mine[0], ref[0]))
+    finite = [(a, b) for a, b in zip(mine[1], ref[1]) if math.isfinite(b)]
+    assert len(finite) == 29 and not math.isfinite(mine[1][8])
+    worst_norm = max(abs(a - b) / abs(b) for a, b in finite)
+    worst_param = _worst_param(ref_model, my_model)
+    log(f"[accumulation loop] worst rel: loss {worst_loss:.2e} norm {worst_norm:.2e} param {worst_param:.2e}")
     assert worst_loss <= 1e-6 and worst_norm <= 1e-6 and worst_param <= 1e-5
     assert my_opt._engine.error_flag() == 0
