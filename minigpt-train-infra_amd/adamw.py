@@ -146,9 +146,11 @@ class _TrackedState(defaultdict):
         self._owner = weakref.ref(owner)
 
     def __missing__(self, key):
-        # torch's _init_group reads state[p] for a parameter without state
+        # torch's _init_group reads state[p] for a parameter without state.  An
+        # empty entry means no state, so creating one needs no copy; a later
+        # write into it marks the optimizer.
         entry = _TrackedEntry(self._owner)
-        self[key] = entry
+        dict.__setitem__(self, key, entry)
         return entry
 
     def entry(self, values: dict) -> _TrackedEntry:

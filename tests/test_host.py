@@ -280,8 +280,9 @@ def test_writes_into_a_state_entry_mark_the_optimizer(mg):
 
     p = nn.Parameter(torch.zeros(4))
     opt = mg.AdamW([p])
+    opt._state_dirty = False
     e = opt.state[p]                     # torch's _init_group creates the entry this way
-    assert isinstance(e, dict) and len(e) == 0
+    assert isinstance(e, dict) and len(e) == 0 and not opt._state_dirty
     e["step"] = torch.tensor(0.0)
     writes = [
         lambda: e.__setitem__("step", torch.tensor(1.0)),
