@@ -308,7 +308,9 @@ def test_writes_into_a_state_entry_mark_the_optimizer(mg):
 
 def test_state_dict_loads_with_weights_only(mg):
     """state_dict() entries are plain dicts, so a checkpoint holding them
-    loads with torch.load(weights_only=True), which refuses other classes."""
+    loads with torch.load(weights_only=True), which refuses other classes.
+    The reference's loader (src/minigpt/checkpoint.py:132) calls torch.load
+    without the argument, and torch 2.10's default is weights_only=True."""
     import io
 
     p = nn.Parameter(torch.zeros(3))
