@@ -17,14 +17,13 @@ importlib.import_module("minigpt-train-infra_amd").
 
 from .adamw import AdamW
 from .clip_grad import clip_grad_norm_
-from .grad_scaler import GradScaler, OptState
+from .grad_scaler import GradScaler
 from .schedule import build_adamw_param_groups, cosine_lr, optimizer_completed_steps, set_optimizer_lr
 from . import paramsets
 
 __all__ = [
     "AdamW",
     "GradScaler",
-    "OptState",
     "clip_grad_norm_",
     "build_adamw_param_groups",
     "cosine_lr",

@@ -72,25 +72,6 @@ def build_host(verbose: bool = False) -> Path:
     return HOST_DIR / "mgopt_host.so"
 
 
-PROBE_SRC = HERE / "csrc" / "stream_probe.hip"
-PROBE = OUT_DIR / "stream_probe"
-
-
-def build_probe(verbose: bool = False) -> Path:
-    """Builds the streaming-bandwidth probe (a standalone executable that
-    bench.py --stream-probe runs) into _build/."""
-    OUT_DIR.mkdir(exist_ok=True)
-    flags = [f for f in HIPCC_FLAGS if f not in ("-fPIC", "-shared", "-fvisibility=hidden")]
-    cmd = [hipcc(), *flags, str(PROBE_SRC), "-o", str(PROBE)]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}")
-    return PROBE
-
-
 if __name__ == "__main__":
     print(build(verbose=True))
     print(build_host(verbose=False))
-    print(build_probe(verbose=False))

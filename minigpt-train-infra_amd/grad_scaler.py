@@ -16,23 +16,28 @@ What differs is where the work happens:
 from __future__ import annotations
 
 import ctypes
-from collections import abc, defaultdict
-from enum import Enum
-from typing import Any, Iterable
+from collections import abc
+from typing import Any
 
 import torch
 
 from . import _native as N
 
-
-class OptState(Enum):
-    READY = 0
-    UNSCALED = 1
-    STEPPED = 2
+#: the keys of a GradScaler state dict, in torch's order (the checkpoint
+#: format of src/minigpt/checkpoint.py:40-42 and src/minigpt/optim.py:254-273)
+_STATE_KEYS = ("scale", "growth_factor", "backoff_factor", "growth_interval", "_growth_tracker")
 
 
-def _refresh_per_optimizer_state() -> dict[str, Any]:
-    return {"stage": OptState.READY, "found_inf_per_device": {}}
+class _Iteration:
+    """What this scaler has done to one optimizer since the last update():
+    whether unscale_ and step ran, and the device flag the norm pass fills."""
+
+    __slots__ = ("unscaled", "stepped", "found_inf")
+
+    def __init__(self) -> None:
+        self.unscaled = False
+        self.stepped = False
+        self.found_inf: torch.Tensor | None = None
 
 
 class GradScaler:
@@ -47,23 +52,31 @@ class GradScaler:
     ) -> None:
         self._device = device
         self._enabled = enabled
-        if self._enabled:
-            if device != "cuda":
-                raise RuntimeError("this GradScaler runs on the GPU only (device='cuda'); there is no CPU path")
-            if not torch.cuda.is_available():
-                raise RuntimeError("GradScaler is enabled but no ROCm GPU is visible")
-            if not growth_factor > 1.0:
-                raise AssertionError("The growth factor must be > 1.0.")
-            if not backoff_factor < 1.0:
-                raise AssertionError("The backoff factor must be < 1.0.")
-            self._init_scale = init_scale
-            self._scale: torch.Tensor | None = None
-            self._growth_factor = growth_factor
-            self._backoff_factor = backoff_factor
-            self._growth_interval = growth_interval
-            self._init_growth_tracker = 0
-            self._growth_tracker: torch.Tensor | None = None
-            self._per_optimizer_states: dict[int, dict[str, Any]] = defaultdict(_refresh_per_optimizer_state)
+        self._iters: dict[int, _Iteration] = {}
+        if not enabled:
+            return
+        if device != "cuda":
+            raise RuntimeError("this GradScaler runs on the GPU only (device='cuda'); there is no CPU path")
+        if not torch.cuda.is_available():
+            raise RuntimeError("GradScaler is enabled but no ROCm GPU is visible")
+        if not growth_factor > 1.0:
+            raise AssertionError("The growth factor must be > 1.0.")
+        if not backoff_factor < 1.0:
+            raise AssertionError("The backoff factor must be < 1.0.")
+        self._growth_factor = growth_factor
+        self._backoff_factor = backoff_factor
+        self._growth_interval = growth_interval
+        # values the device scalars start from when scale() first creates them
+        self._init_scale = init_scale
+        self._init_growth_tracker = 0
+        self._scale: torch.Tensor | None = None
+        self._growth_tracker: torch.Tensor | None = None
+
+    def _iteration(self, optimizer) -> _Iteration:
+        rec = self._iters.get(id(optimizer))
+        if rec is None:
+            rec = self._iters[id(optimizer)] = _Iteration()
+        return rec
 
     # --------------------------------------------------------------- scale
     def _check_scale_growth_tracker(self, funcname: str) -> tuple[torch.Tensor, torch.Tensor]:
@@ -79,27 +92,24 @@ class GradScaler:
         self._growth_tracker = torch.full((), self._init_growth_tracker, dtype=torch.int32, device=dev)
 
     def scale(self, outputs):
-        """outputs * scale (grad_scaler.py:190-233)."""
+        """outputs * scale, for a tensor or a (nested) list/tuple/iterable of
+        them (grad_scaler.py:190-233); the scale and growth tracker are created
+        on the first tensor's device."""
         if not self._enabled:
             return outputs
-        if isinstance(outputs, torch.Tensor):
+        return self._scaled(outputs)
+
+    def _scaled(self, x):
+        if isinstance(x, torch.Tensor):
             if self._scale is None:
-                self._lazy_init_scale_growth_tracker(outputs.device)
-            return outputs * self._scale.to(device=outputs.device, non_blocking=True)
-
-        def apply(val):
-            if isinstance(val, torch.Tensor):
-                if self._scale is None:
-                    self._lazy_init_scale_growth_tracker(val.device)
-                return val * self._scale.to(device=val.device, non_blocking=True)
-            if isinstance(val, abc.Iterable):
-                mapped = map(apply, val)
-                if isinstance(val, (list, tuple)):
-                    return type(val)(mapped)
-                return mapped
-            raise ValueError("outputs must be a Tensor or an iterable of Tensors")
-
-        return apply(outputs)
+                self._lazy_init_scale_growth_tracker(x.device)
+            s = self._scale if self._scale.device == x.device else self._scale.to(x.device, non_blocking=True)
+            return x * s
+        if isinstance(x, (list, tuple)):
+            return type(x)(self._scaled(v) for v in x)
+        if isinstance(x, abc.Iterable):
+            return map(self._scaled, x)
+        raise ValueError("outputs must be a Tensor or an iterable of Tensors")
 
     def _engine_of(self, optimizer) -> Any:
         get = getattr(optimizer, "_get_engine", None)
@@ -115,15 +125,13 @@ class GradScaler:
         if not self._enabled:
             return
         self._check_scale_growth_tracker("unscale_")
-        state = self._per_optimizer_states[id(optimizer)]
-        if state["stage"] is OptState.UNSCALED:
+        rec = self._iteration(optimizer)
+        if rec.unscaled and not rec.stepped:
             raise RuntimeError("unscale_() has already been called on this optimizer since the last update().")
-        if state["stage"] is OptState.STEPPED:
+        if rec.stepped:
             raise RuntimeError("unscale_() is being called after step().")
-        engine = self._engine_of(optimizer)
-        found_inf = engine.request_unscale(self._scale)
-        state["found_inf_per_device"] = {found_inf.device: found_inf}
-        state["stage"] = OptState.UNSCALED
+        rec.found_inf = self._engine_of(optimizer).request_unscale(self._scale)
+        rec.unscaled = True
 
     # ---------------------------------------------------------------- step
     def step(self, optimizer, *args: Any, **kwargs: Any):
@@ -134,13 +142,13 @@ class GradScaler:
         if "closure" in kwargs:
             raise RuntimeError("Closure use is not currently supported if GradScaler is enabled.")
         self._check_scale_growth_tracker("step")
-        state = self._per_optimizer_states[id(optimizer)]
-        if state["stage"] is OptState.STEPPED:
+        rec = self._iteration(optimizer)
+        if rec.stepped:
             raise RuntimeError("step() has already been called since the last update().")
-        if state["stage"] is OptState.READY:
+        if not rec.unscaled:
             self.unscale_(optimizer)
         retval = optimizer.step(*args, **kwargs)
-        state["stage"] = OptState.STEPPED
+        rec.stepped = True
         return retval
 
     # -------------------------------------------------------------- update
@@ -162,9 +170,7 @@ class GradScaler:
                 assert new_scale.requires_grad is False, reason
                 _scale.copy_(new_scale)
         else:
-            found = [
-                f for s in self._per_optimizer_states.values() for f in s["found_inf_per_device"].values()
-            ]
+            found = [rec.found_inf for rec in self._iters.values() if rec.found_inf is not None]
             if not found:
                 raise AssertionError("No inf checks were recorded prior to update.")
             if len(found) > 8:
@@ -181,7 +187,7 @@ class GradScaler:
                 ),
                 "mgopt_scaler_update",
             )
-        self._per_optimizer_states = defaultdict(_refresh_per_optimizer_state)
+        self._iters = {}
 
     # ------------------------------------------------------------ accessors
     def _get_scale_async(self) -> torch.Tensor | None:
@@ -191,7 +197,8 @@ class GradScaler:
         """{device: found_inf} recorded by unscale_ for this optimizer
         (grad_scaler.py:465-467): a device tensor that the coming norm pass
         fills, 1.0 when a scaled gradient is inf or NaN."""
-        return self._per_optimizer_states[id(optimizer)]["found_inf_per_device"]
+        rec = self._iters.get(id(optimizer))
+        return {} if rec is None or rec.found_inf is None else {rec.found_inf.device: rec.found_inf}
 
     def get_scale(self) -> float:
         if self._enabled:
@@ -225,48 +232,47 @@ class GradScaler:
         return self._enabled
 
     def state_dict(self) -> dict[str, Any]:
-        if self._enabled:
-            return {
-                "scale": self.get_scale(),
-                "growth_factor": self._growth_factor,
-                "backoff_factor": self._backoff_factor,
-                "growth_interval": self._growth_interval,
-                "_growth_tracker": self._get_growth_tracker(),
-            }
-        return {}
+        """The five values of torch's GradScaler state dict (plain Python
+        numbers, so torch.load(weights_only=True) reads them back); {} when
+        disabled."""
+        if not self._enabled:
+            return {}
+        values = (self.get_scale(), self._growth_factor, self._backoff_factor, self._growth_interval,
+                  self._get_growth_tracker())
+        return dict(zip(_STATE_KEYS, values))
 
     def load_state_dict(self, state_dict: dict[str, Any]) -> None:
         if not self._enabled:
             return
-        if len(state_dict) == 0:
+        if not state_dict:
             raise RuntimeError(
                 "The source state dict is empty, possibly because it was saved "
                 "from a disabled instance of GradScaler."
             )
-        self._init_scale = float(state_dict["scale"])
+        scale, growth, backoff, interval, tracker = (state_dict[k] for k in _STATE_KEYS)
+        self._growth_factor, self._backoff_factor = float(growth), float(backoff)
+        self._growth_interval = int(interval)
+        self._init_scale, self._init_growth_tracker = float(scale), int(tracker)
+        # device scalars that already exist take the values in place (a
+        # captured or recorded pointer to them stays valid)
         if self._scale is not None:
-            self._scale.fill_(state_dict["scale"])
-        self._growth_factor = float(state_dict["growth_factor"])
-        self._backoff_factor = float(state_dict["backoff_factor"])
-        self._growth_interval = int(state_dict["growth_interval"])
-        self._init_growth_tracker = int(state_dict["_growth_tracker"])
+            self._scale.fill_(self._init_scale)
         if self._growth_tracker is not None:
-            self._growth_tracker.fill_(state_dict["_growth_tracker"])
+            self._growth_tracker.fill_(self._init_growth_tracker)
 
     def __getstate__(self) -> dict[str, Any]:
-        state = self.__dict__.copy()
+        # Device scalars and pointer caches stay behind: the unpickled scaler
+        # recreates its scalars from the current values at its next scale().
+        if self._enabled and self._iters:
+            raise AssertionError(
+                "A GradScaler instance may only be pickled at the beginning "
+                "of an iteration, or at the end after scaler.update()."
+            )
+        transient = ("_found_ptrs", "_found_arr")
+        state = {k: v for k, v in self.__dict__.items() if k not in transient}
         if self._enabled:
-            if len(self._per_optimizer_states) != 0:
-                raise AssertionError(
-                    "A GradScaler instance may only be pickled at the beginning "
-                    "of an iteration, or at the end after scaler.update()."
-                )
-            state["_init_scale"] = self.get_scale()
-            state["_init_growth_tracker"] = self._get_growth_tracker()
-            state["_scale"] = None
-            state["_growth_tracker"] = None
-        state.pop("_found_ptrs", None)   # device addresses and a ctypes array: not part of the state
-        state.pop("_found_arr", None)
+            state.update(_init_scale=self.get_scale(), _init_growth_tracker=self._get_growth_tracker(),
+                         _scale=None, _growth_tracker=None)
         return state
 
     def __setstate__(self, state: dict[str, Any]) -> None:
