@@ -20,7 +20,6 @@ import importlib
 import json
 import math
 import os
-import subprocess
 import sys
 import time
 from pathlib import Path
@@ -56,6 +55,24 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+# Above this many tensors the synthetic values are written by one generator
+# launch into a staging buffer and copied in by multi-tensor copies, instead of
+# one launch per tensor: the 20,000-tensor set then takes a few hundred set-up
+# dispatches instead of 40,000.  The tensors stay separate allocations.
+MANY_TENSORS = 1000
+
+
+def fill_tensors(tensors: list[torch.Tensor], seed: int, stream_of, sigma: float) -> None:
+    """Synthetic values for a list of tensors: tensor i from stream
+    stream_of(i), or, for long lists, all of them from stream stream_of(0)
+    through one staging fill."""
+    if len(tensors) > MANY_TENSORS:
+        syn.fill_many_(tensors, seed, stream_of(0), sigma)
+    else:
+        for i, t in enumerate(tensors):
+            syn.fill_(t, seed, stream_of(i), sigma)
+
+
 def build_workload(name: str, dev: torch.device, param_dtype: str | None = None):
     spec = dict(WORKLOADS[name])
     if param_dtype is not None:
@@ -64,11 +81,9 @@ def build_workload(name: str, dev: torch.device, param_dtype: str | None = None)
     decay = [(n, s) for n, s in shapes if len(s) >= 2]
     nodecay = [(n, s) for n, s in shapes if len(s) < 2]
     ordered = decay + nodecay
-    params = []
-    for i, (_, s) in enumerate(ordered):
-        p = torch.empty(s, dtype=DT[spec["param"]], device=dev)
-        syn.fill_(p, syn.PARAM_SEED, syn.param_stream(i), 0.02)
-        params.append(torch.nn.Parameter(p))
+    raw = [torch.empty(s, dtype=DT[spec["param"]], device=dev) for _, s in ordered]
+    fill_tensors(raw, syn.PARAM_SEED, syn.param_stream, 0.02)
+    params = [torch.nn.Parameter(p) for p in raw]
     groups = [
         {"params": params[: len(decay)], "param_names": [n for n, _ in decay], "group_name": "decay", "weight_decay": 0.1},
         {"params": params[len(decay):], "param_names": [n for n, _ in nodecay], "group_name": "no_decay", "weight_decay": 0.0},
@@ -136,6 +151,34 @@ def read_traffic(name: str) -> float | None:
     return None
 
 
+def time_device_copy(dev: torch.device, gib: float, stream, launches: int = 6) -> dict:
+    """The runtime's device-to-device copy (torch's copy_ -> hipMemcpyAsync,
+    run as the runtime's own copy kernel) of one `gib`-GiB buffer into
+    another, timed with HIP events on `stream`; the first launch is untimed.
+    Bytes moved per launch: the buffer read once and written once."""
+    n = int(gib * (1 << 30)) // 4
+    src = torch.empty(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    src.fill_(1.0)
+    dst.copy_(src)
+    spans = []
+    for _ in range(launches):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        dst.copy_(src)
+        b.record(stream)
+        spans.append((a, b))
+    torch.cuda.synchronize()
+    ms = sorted(a.elapsed_time(b) for a, b in spans)
+    moved = 2 * 4 * n
+    med = ms[len(ms) // 2]
+    out = {"bytes_per_launch": moved, "launches": launches, "ms": med, "ms_all": ms, "GBps": moved / (med * 1e-3) / 1e9}
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
 def vs_torch(name: str, steps: int, warmup: int, dev: torch.device) -> dict:
     """The reference's own GPU path on this GPU, beside this package, on the
     same fp32 parameters and gradients.  On a cuda device the reference's
@@ -153,10 +196,10 @@ def vs_torch(name: str, steps: int, warmup: int, dev: torch.device) -> dict:
     stream = torch.cuda.current_stream(dev)
 
     def refill(step: int) -> None:
-        for i, p in enumerate(params):
+        for p in params:
             if p.grad is None:
                 p.grad = torch.empty_like(p)
-            syn.fill_(p.grad, syn.GRAD_SEED, syn.grad_stream(step, i), 1e-3 * init_scale)
+        fill_tensors([p.grad for p in params], syn.GRAD_SEED, lambda i: syn.grad_stream(step, i), 1e-3 * init_scale)
 
     def torch_groups():
         return [{k: v for k, v in g.items()} for g in groups]
@@ -215,10 +258,13 @@ def main() -> int:
     ap.add_argument("--vs-torch", action="store_true",
                     help="instead of the benchmark line, time torch's own GPU path (the reference's fused AdamW + "
                          "GradScaler + clip_grad_norm_) beside this package on fp32 params and grads of the workload")
-    ap.add_argument("--stream-probe", action="store_true",
-                    help="instead of the benchmark line, run the streaming-bandwidth probe (kernels with pass 2's "
-                         "launch shape: read, write, copy, three streams in place, pass 2's byte mix) and print "
-                         "its JSON lines")
+    ap.add_argument("--graph", action="store_true",
+                    help="AdamW(capturable=True): capture the whole step in one HIP graph after the warm-up and "
+                         "time its replays (for small sets, whose eager step is bound by the host's launches)")
+    ap.add_argument("--copy-ceiling", type=float, default=0.0, metavar="GIB",
+                    help="after the timed steps, also time the runtime's own device-to-device copy "
+                         "(hipMemcpyAsync, torch's copy_) of a GIB-gibibyte buffer in this process, "
+                         "and report pass 2's rate against it")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB fp32 device copy (reads 1 GiB, writes 1 GiB) three times, "
                          "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -227,12 +273,6 @@ def main() -> int:
         print("bench.py measures one GPU only: the optimizer step here has no multi-GPU path (use --gpus 1)", file=sys.stderr)
         return 2
 
-    if args.stream_probe:
-        # a child process (it initialises the GPU itself); this process has not touched the GPU
-        probe = ROOT / PKG_DIR / "_build" / "stream_probe"
-        if not probe.exists():
-            importlib.import_module(f"{PKG_DIR}.build").build_probe()
-        return subprocess.run([str(probe)], check=False).returncode
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.calibrate_copy:
@@ -251,16 +291,17 @@ def main() -> int:
     log(f"workload {args.workload}: {len(params)} tensors, {n_params:,} params ({spec['param']} params, {spec['grad']} grads)")
 
     init_scale = 65536.0
-    opt = mg.AdamW(groups, lr=3e-4, betas=(0.9, 0.95), eps=1e-8)
+    opt = mg.AdamW(groups, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, capturable=args.graph)
     scaler = mg.GradScaler("cuda", init_scale=init_scale, growth_factor=2.0, backoff_factor=0.5, growth_interval=2000)
     scaler.scale(torch.ones((), device=dev))
+    grads = [torch.empty(p.shape, dtype=DT[spec["grad"]], device=dev) for p in params]
+    fill_tensors(grads, syn.GRAD_SEED, lambda i: syn.grad_stream(1, i), 1e-3 * init_scale)
     if spec["grad"] == spec["param"]:
-        for i, p in enumerate(params):
-            p.grad = syn.fill_(torch.empty_like(p), syn.GRAD_SEED, syn.grad_stream(1, i), 1e-3 * init_scale)
+        for p, g in zip(params, grads):
+            p.grad = g
     else:
-        grads = [syn.fill_(torch.empty(p.shape, dtype=DT[spec["grad"]], device=dev), syn.GRAD_SEED,
-                           syn.grad_stream(1, i), 1e-3 * init_scale) for i, p in enumerate(params)]
         opt.set_grad_source(grads)
+    del grads
     eng = opt._get_engine()
     torch.cuda.synchronize()
     log(f"resident: {torch.cuda.memory_allocated(dev) / 1e9:.1f} GB (parameters, gradients, optimizer state)")
@@ -288,27 +329,58 @@ def main() -> int:
     for _ in range(args.warmup):
         one_step(False)
     torch.cuda.synchronize()
+    if args.graph:
+        # the whole step (unscale_, clip_grad_norm_, step, update) in one HIP
+        # graph; each timed step refreshes the learning rate and replays it
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            scaler.unscale_(opt)
+            mg.clip_grad_norm_(params, 1.0)
+            scaler.step(opt)
+            scaler.update()
+
+        def one_step(record: bool) -> None:
+            mg.set_optimizer_lr(opt, 3e-4)
+            if record:
+                a = torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+            graph.replay()
+            if record:
+                b = torch.cuda.Event(enable_timing=True)
+                b.record(stream)
+                ev["adamw"].append((a, b))
+
+        one_step(False)
+        torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         one_step(True)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     step_s = (t1 - t0) / args.steps
-    skipped = int(round(args.steps + args.warmup - float(eng.steps.max())))
-    if eng.error_flag() != 0 or skipped != 0:
-        log(f"error flag {eng.error_flag()}, skipped {skipped}")
+    taken = args.steps + args.warmup + (1 if args.graph else 0)
+    skipped = int(round(taken - float(eng.steps.max())))
+    if eng.device_bc_flag() != 0 or skipped != 0:
+        log(f"bias corrections evaluated on the device: {eng.device_bc_flag()}, skipped {skipped}")
         return 1
-    norm_ms = sum(a.elapsed_time(b) for a, b in ev["norm"]) / len(ev["norm"])
+    # graph mode: one replay holds both passes, so "adamw" times the whole step
+    norm_ms = sum(a.elapsed_time(b) for a, b in ev["norm"]) / len(ev["norm"]) if ev["norm"] else 0.0
     adamw_ms = sum(a.elapsed_time(b) for a, b in ev["adamw"]) / len(ev["adamw"])
 
     bpp = BYTES_PER_PARAM[(spec["param"], spec["grad"])]
     grad_bytes = 2 if spec["grad"] != "f32" else 4
     achieved_step = bpp * n_params / step_s / 1e9
     adamw_gbps = bpp * n_params / (adamw_ms * 1e-3) / 1e9
-    norm_gbps = grad_bytes * n_params / (norm_ms * 1e-3) / 1e9
+    norm_gbps = grad_bytes * n_params / (norm_ms * 1e-3) / 1e9 if norm_ms else 0.0
     log(f"step {step_s*1e3:.3f} ms ({1/step_s:.2f} steps/s); compulsory {bpp} B/param -> {achieved_step:.0f} GB/s "
         f"({100*achieved_step/HBM_PEAK_GBPS:.1f}% of peak); norm pass {norm_ms:.3f} ms ({norm_gbps:.0f} GB/s), "
         f"AdamW pass {adamw_ms:.3f} ms ({adamw_gbps:.0f} GB/s)")
+
+    copy = None
+    if args.copy_ceiling > 0:
+        copy = time_device_copy(dev, args.copy_ceiling, stream)
+        log(f"runtime copy of {args.copy_ceiling:g} GiB: {copy['ms']:.3f} ms = {copy['GBps']:.0f} GB/s "
+            f"(read + write); pass 2 runs at {adamw_gbps / copy['GBps']:.3f} of it")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -341,7 +413,8 @@ def main() -> int:
             "param_dtype": spec["param"],
             "grad_dtype": spec["grad"],
             "state": "fp32 master/exp_avg/exp_avg_sq" if spec["param"] != "f32" else "fp32 exp_avg/exp_avg_sq",
-            "step": "GradScaler.unscale_ + clip_grad_norm_(1.0) + AdamW + GradScaler.update",
+            "step": "GradScaler.unscale_ + clip_grad_norm_(1.0) + AdamW + GradScaler.update"
+                    + (", captured in one HIP graph and replayed (AdamW capturable=True)" if args.graph else ""),
             "parallelism": "single GPU",
         },
         "achieved_GBps": achieved_step,
@@ -351,7 +424,7 @@ def main() -> int:
         "implementation_bytes_per_param": bpp + grad_bytes,
         "implementation_GBps": (bpp + grad_bytes) * n_params / step_s / 1e9,
         "skipped_steps": skipped,
-        "passes_ms": {"norm": norm_ms, "adamw": adamw_ms},
+        "passes_ms": {"graph_replay": adamw_ms} if args.graph else {"norm": norm_ms, "adamw": adamw_ms},
         "roofline": {
             "bound": "hbm",
             "achieved": adamw_gbps,
@@ -362,6 +435,9 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
     }
+    if copy is not None:
+        copy["adamw_frac_of_copy"] = adamw_gbps / copy["GBps"]
+        out["copy_ceiling"] = copy
     print(json.dumps(out), flush=True)
     return 0
 

@@ -47,7 +47,9 @@ extern "C" {
 #define MGOPT_MAX_GROUPS 16
 
 /* flags for mgopt_adamw_step */
-#define MGOPT_WRITEBACK_GRADS 1 /* store the unscaled, clipped gradient back into each grad */
+#define MGOPT_WRITEBACK_GRADS 1  /* store the unscaled, clipped gradient back into each grad */
+#define MGOPT_GROUPS_ON_DEVICE 2 /* `groups` is a device pointer, read by the kernel when it runs (so a
+                                    launch captured in a HIP graph picks up the values current at replay) */
 
 /* One parameter tensor of the optimizer (one entry of torch.optim.Optimizer's
  * param_groups[*]["params"], torch/optim/optimizer.py:164-189).
@@ -112,7 +114,8 @@ MGOPT_API int mgopt_plan_set_grads(mgopt_plan* plan, const void* const* grads_ho
  *   torch._amp_foreach_non_finite_check_and_unscale_ (torch/amp/grad_scaler.py:280-284),
  *   torch._foreach_norm + vector_norm(stack)       (torch/nn/utils/clip_grad.py:96-108),
  *   the clip coefficient                           (clip_grad.py:165-169).
- * Reads every grad once.  scale_dev: the GradScaler scale (fp32 scalar); when
+ * Reads every grad once (one pass-1 launch per gradient dtype, then one
+ * finalize launch).  scale_dev: the GradScaler scale (fp32 scalar); when
  * non-NULL each grad element g becomes float(g) * float(1/double(scale))
  * before squaring, and found_inf_dev receives 1.0 if any *input* element is
  * non-finite, else 0.0.  coef_dev (when non-NULL) receives the clip
@@ -126,10 +129,19 @@ MGOPT_API int mgopt_grad_norm(mgopt_plan* plan, const float* scale_dev, double m
  *   GradScaler.step's skip decision  (torch/amp/grad_scaler.py:348-358, 403-454),
  *   clip_grad.py:174 (_foreach_mul_ by the clip coefficient),
  *   torch/optim/adam.py:347-552 (_single_tensor_adam) / 803-899 (_fused_adam).
- * groups: n_groups hyper-parameter sets (host memory, passed by value to the
- * kernel).  bc_dev: double table bc[(group * bc_cap + t) * 2 + {0,1}] =
- * {1 - beta1**t, (1 - beta2**t) ** 0.5} computed on the host with the same
- * expressions as adam.py:529-536; it must cover every reachable t.
+ * groups: n_groups hyper-parameter sets, passed by value to the kernel, or,
+ * with MGOPT_GROUPS_ON_DEVICE in flags, a device array of them that the kernel
+ * reads when it runs.  bc_dev: double table bc[(group * bc_cap + t) * 2 + {0,1}]
+ * = {1 - beta1**t, (1 - beta2**t) ** 0.5} for 1 <= t < bc_cap, computed on the
+ * host with the same expressions as adam.py:529-536, and {beta1, beta2} at
+ * t = 0 (the betas the row was computed for).  A step count that is not an
+ * integer in [1, bc_cap) -- one written into the state, or reached by graph
+ * replays -- or a group whose betas differ from its row's, takes the same
+ * expressions evaluated on the device in double (the device
+ * pow can differ from the host's by an ulp of the double), and raises the
+ * plan's flag (mgopt_plan_flags).  A prologue launch (one thread per tensor)
+ * advances the step counts and forms each tensor's fp32 constants; pass 2
+ * then reads them once per work-group.
  * scale_dev (nullable): unscale as in mgopt_grad_norm.  coef_dev (nullable):
  * clip coefficient.  found_inf_dev (nullable): nonzero skips the whole step,
  * leaving params, moments and step counts untouched. */
@@ -160,10 +172,11 @@ MGOPT_API int mgopt_sync_master(mgopt_plan* plan, void* stream);
  * skip bookkeeping of train.py:487-489,501-507. */
 MGOPT_API int mgopt_plan_set_window(mgopt_plan* plan, void* window_dev);
 
-/* Blocking read of the plan's device error flag: nonzero when a pass-2
- * work-group met a step count outside the bias-correction table and left its
- * tensor untouched.  No reference counterpart (a safety net of this engine). */
-MGOPT_API int mgopt_plan_error_flag(mgopt_plan* plan, int* out);
+/* Blocking read of the plan's device flag: nonzero once a pass-2 work-group
+ * has computed its bias corrections on the device because its step count was
+ * outside the bias-correction table (see mgopt_adamw_step).  No reference
+ * counterpart. */
+MGOPT_API int mgopt_plan_flags(mgopt_plan* plan, int* out);
 
 /* Deterministic test data: dst[i] = synth(key(seed, stream_id), i) in dtype
  * (MGOPT_F32/F16/BF16).  No reference counterpart; used by tests and the

@@ -16,6 +16,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_build" / "libmgopt.so"
 F32, F16, BF16, NONE = 0, 1, 2, -1
 MAX_GROUPS = 16
 WRITEBACK_GRADS = 1
+GROUPS_ON_DEVICE = 2
 
 #: every symbol include/mgopt.h declares
 EXPORTS = (
@@ -29,7 +30,7 @@ EXPORTS = (
     "mgopt_scale_grads",
     "mgopt_sync_master",
     "mgopt_plan_set_window",
-    "mgopt_plan_error_flag",
+    "mgopt_plan_flags",
     "mgopt_synth_fill",
     "mgopt_last_error",
     "mgopt_version",
@@ -78,12 +79,12 @@ def _declare(lib: ctypes.CDLL) -> None:
         "mgopt_plan_num_chunks": (i64, [vp]),
         "mgopt_plan_set_grads": (ctypes.c_int, [vp, ctypes.POINTER(vp), vp]),
         "mgopt_grad_norm": (ctypes.c_int, [vp, vp, dbl, vp, vp, vp, vp]),
-        "mgopt_adamw_step": (ctypes.c_int, [vp, ctypes.POINTER(GroupHparams), vp, i64, vp, vp, vp, i32, vp]),
+        "mgopt_adamw_step": (ctypes.c_int, [vp, vp, vp, i64, vp, vp, vp, i32, vp]),
         "mgopt_scaler_update": (ctypes.c_int, [vp, vp, ctypes.POINTER(vp), i32, dbl, dbl, i32, vp]),
         "mgopt_scale_grads": (ctypes.c_int, [vp, vp, vp]),
         "mgopt_sync_master": (ctypes.c_int, [vp, vp]),
         "mgopt_plan_set_window": (ctypes.c_int, [vp, vp]),
-        "mgopt_plan_error_flag": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_int)]),
+        "mgopt_plan_flags": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_int)]),
         "mgopt_synth_fill": (ctypes.c_int, [vp, i32, i64, u64, u64, dbl, u64, dbl, vp]),
         "mgopt_last_error": (ctypes.c_char_p, []),
         "mgopt_version": (ctypes.c_char_p, []),

@@ -26,6 +26,7 @@ from collections import defaultdict
 from itertools import chain
 from typing import Any, Iterable
 
+import numpy as np
 import torch
 from torch.optim import optimizer as _torch_optimizer
 from torch.utils.weak import WeakIdKeyDictionary
@@ -84,6 +85,20 @@ def _call_with_hooks(func, self, args, kwargs):
         for hook in chain(self._optimizer_step_post_hooks.values(), post.values()):
             hook(self, args, kwargs)
     return out
+
+
+class _GradMark:
+    """Post-accumulate-grad hook of a parameter backed by the gradient arena:
+    records that its gradient exists.  Holds only the record, not the
+    optimizer."""
+
+    __slots__ = ("present", "i")
+
+    def __init__(self, present: np.ndarray, i: int):
+        self.present, self.i = present, i
+
+    def __call__(self, param) -> None:
+        self.present[self.i] = 1
 
 
 class _TrackedEntry(dict):
@@ -205,6 +220,14 @@ class AdamW(torch.optim.Optimizer):
         .grad during the step (the reference leaves them in .grad;
         train.py never reads them after the step, so this is off by default).
     chunk_elems: elements per pass-2 work-group (a multiple of 512).
+
+    capturable=True (torch/optim/adam.py:163-176, 343-346): step() may be
+    captured in a HIP graph (torch.cuda.graph) together with the scaler's
+    unscale_/step/update and clip_grad_norm_, and replayed.  The kernels then
+    read the groups' hyper-parameters from device memory (refresh_hparams, or
+    set_optimizer_lr, brings them up to date before a replay) and the step
+    counts and bias corrections from device memory; gradients must stay in
+    the same buffers as at capture.  Run one step outside capture first.
     """
 
     # GradScaler.step hands found_inf/grad_scale to the optimizer instead of
@@ -245,8 +268,6 @@ class AdamW(torch.optim.Optimizer):
             raise NotImplementedError("amsgrad is not supported by this AdamW")
         if differentiable:
             raise NotImplementedError("differentiable=True is not supported by this AdamW")
-        if capturable:
-            raise NotImplementedError("capturable=True (graph capture of the step) is not supported by this AdamW")
         defaults = dict(
             lr=lr,
             betas=betas,
@@ -273,7 +294,13 @@ class AdamW(torch.optim.Optimizer):
     # ----------------------------------------------------------- internals
     def _get_engine(self) -> _Engine:
         if self._engine is None:
-            self._engine = _Engine(self, self._master_weights, self._chunk_elems)
+            if torch.cuda.is_current_stream_capturing():
+                # creating the engine allocates device and pinned host memory
+                # and uploads its tables, none of which a graph can record
+                raise RuntimeError("this optimizer has not stepped yet: run one step outside graph capture "
+                                   "before capturing")
+            capturable = bool(self.defaults.get("capturable")) or any(g.get("capturable") for g in self.param_groups)
+            self._engine = _Engine(self, self._master_weights, self._chunk_elems, capturable=capturable)
         return self._engine
 
     def _reconcile_state(self) -> None:
@@ -382,10 +409,14 @@ class AdamW(torch.optim.Optimizer):
                 loss = closure()
         eng = self._get_engine()
         if torch.cuda.is_current_stream_capturing():
-            # as torch's non-capturable optimizers refuse (optimizer.py:451-478):
-            # a replay would reuse this step's learning rate and host-side state
-            raise RuntimeError("Attempting graph capture of step() for an instance of this AdamW, which runs with "
-                               "capturable=False: the learning rate and step bookkeeping are host-side")
+            if not eng.capturable:
+                # as torch's non-capturable optimizers refuse (optimizer.py:451-478):
+                # a replay would reuse this step's learning rate and host-side state
+                raise RuntimeError("Attempting graph capture of step() for an instance of this AdamW, which runs "
+                                   "with capturable=False: the learning rate and step bookkeeping are host-side")
+            if self._state_dirty:
+                raise RuntimeError("optimizer state was written since the last step; run one step outside graph "
+                                   "capture first")
         if self._state_dirty:
             with torch.no_grad():
                 self._reconcile_state()
@@ -406,11 +437,15 @@ class AdamW(torch.optim.Optimizer):
     def zero_grad(self, set_to_none: bool = True) -> None:
         arena = getattr(self, "_grad_arena", None)
         if arena is not None:
-            # the arena persists: one fill, and every p.grad is (again) its view
+            # the arena persists: one fill, and every p.grad is (again) its view;
+            # set_to_none=True forgets which gradients exist, as torch's None does
             arena.zero_()
-            for p, g in zip(self._get_engine().params, self._grad_views):
+            eng = self._get_engine()
+            for p, g in zip(eng.params, self._grad_views):
                 if p.grad is not g:
                     p.grad = g
+            if set_to_none and eng.present is not None:
+                eng.present[:] = 0
         elif set_to_none and self._engine is not None and self._engine.grad_source is None:
             # the per-parameter `p.grad = None` loop of Optimizer.zero_grad, done natively
             # (3.4 ms of Python at 20,000 parameters)
@@ -420,14 +455,25 @@ class AdamW(torch.optim.Optimizer):
         if self._engine is not None:
             self._engine.reset_iteration()
 
-    def use_grad_arena(self, dtype: torch.dtype | None = None) -> torch.Tensor:
+    def use_grad_arena(self, dtype: torch.dtype | None = None, track_unused: bool = True) -> torch.Tensor:
         """Backs every parameter's .grad with a view of one flat device buffer
         (segments on 256-byte boundaries, the layout of the moment arenas), so
         gradients are contiguous across the whole parameter set and
         zero_grad() is a single fill whatever set_to_none says; autograd then
         accumulates into the views in place.  dtype: gradient dtype when it
         differs from the parameters' (fp16 gradients for fp32 parameters, for
-        instance; sets each parameter's grad_dtype).  Returns the buffer."""
+        instance; sets each parameter's grad_dtype).  Returns the buffer.
+
+        track_unused (default): a post-accumulate-grad hook on each parameter
+        records which gradients exist in torch's sense, so a parameter that
+        received no gradient since zero_grad(set_to_none=True) is left alone
+        by the step (no update, no state), as torch leaves a parameter whose
+        .grad is None (torch/optim/adam.py:153); zero_grad(set_to_none=False)
+        keeps the record, as torch keeps the zeroed tensors.  The hooks cost
+        about a microsecond per parameter and backward.  track_unused=False:
+        no hooks, and every arena gradient takes part in every step (torch's
+        behaviour when every .grad exists, as after one backward through a
+        model that uses all its parameters with set_to_none=False)."""
         eng = self._get_engine()
         dts = {p.dtype for p in eng.params}
         if dtype is None:
@@ -442,11 +488,21 @@ class AdamW(torch.optim.Optimizer):
             if dtype != p.dtype:
                 p.grad_dtype = dtype
             views.append(arena[off : off + p.numel()].view(p.shape))
+        present = np.array([p.grad is not None for p in eng.params], np.uint8)
         with torch.no_grad():
             for p, g in zip(eng.params, views):
                 if p.grad is not None:
                     g.copy_(p.grad)
                 p.grad = g
+        for h in getattr(self, "_arena_hooks", ()):
+            h.remove()
+        self._arena_hooks = []
+        if track_unused:
+            for i, p in enumerate(eng.params):
+                self._arena_hooks.append(p.register_post_accumulate_grad_hook(_GradMark(present, i)))
+            eng.present = present
+        else:
+            eng.present = None
         self._grad_arena = arena
         self._grad_views = views
         eng.reset_iteration()
@@ -465,6 +521,15 @@ class AdamW(torch.optim.Optimizer):
         taken.  Replaces the per-step window bookkeeping of train.py:487-489 and
         the optimizer-step difference of train.py:501-507."""
         return self._get_engine().window_metrics(reset)
+
+    def refresh_hparams(self) -> None:
+        """capturable=True: copies the current param_groups values (lr, weight
+        decay, betas, eps) into the device records the kernels read, so that a
+        replay of a captured step uses them.  set_optimizer_lr calls it; call it
+        after any other change to param_groups before a replay.  Asynchronous;
+        a no-op for a non-capturable optimizer or unchanged values."""
+        if self._engine is not None and self._engine.capturable:
+            self._engine.refresh_hparams()
 
     def sync_master_from_params(self) -> None:
         """Re-reads bf16/fp16 parameters into the fp32 master copy (after the

@@ -6,7 +6,9 @@
 //                              fp64 sum of squares -> one partial per chunk
 //   finalize finalize_kernel   one work-group: total norm, clip coefficient,
 //                              found_inf (fixed reduction order: bit-stable)
-//   prologue prologue_kernel   per-tensor step += 1 unless found_inf
+//   prologue prologue_kernel   one thread per tensor: step += 1 unless
+//                              found_inf, then the tensor's fp32 constants
+//                              for pass 2 (bias corrections, step size, decay)
 //   pass 2   adamw_kernel      read grad/param/m/v once, write param/m/v
 //                              (+ bf16/fp16 model copy): unscale, clip, AdamW
 //   update   scaler_kernel     GradScaler scale/growth-tracker state machine
@@ -32,7 +34,7 @@
 
 namespace {
 
-constexpr int kBlock = 512;          // work-group size of pass 1 and the helper kernels
+constexpr int kBlock = 512;          // work-group size of pass 1, finalize and the helper kernels
 // Pass 2 runs one short work-group per chunk.  With the default 1024-element
 // chunks a 512-thread work-group gives one 4-element group to lanes 0-255
 // and lanes 256-511 retire at once: half of a CU's wave slots carry memory
@@ -42,7 +44,6 @@ constexpr int kBlock = 512;          // work-group size of pass 1 and the helper
 // 8.2B set and within 2 % of the best on 124M-2.5B sets.
 constexpr int kAdamBlock = 512;      // work-group size of pass 2
 constexpr size_t kAdamLds = 0;       // LDS bytes reserved per pass-2 work-group (0: no cap on work-groups per CU)
-constexpr int kFinalizeBlock = 1024; // single work-group of the finalize kernel
 constexpr int kVec = 4;              // elements per thread per access: 4 = one 16-B fp32 access per lane;
                                      // 8 (two adjacent 16-B accesses) measured 1.8x slower (32-B lane stride)
 constexpr int kStagingSlots = 4;     // pinned host buffers for grad-pointer uploads
@@ -57,8 +58,10 @@ constexpr bool kNtNormLoad = true;   // nontemporal gradient loads in pass 1
 // one partial per 128K elements.  Pass 1 + finalize measured in one process
 // on the Qwen3-8B set: 16K-element chunks 2.94 ms, 32K 2.50, 64K 2.35,
 // 128K 2.29, 256K 2.31, 512K 2.31; above 128K the smaller sets lose (GPT-2
-// small 0.049 ms at 128K, 0.100 at 512K).  A grid-stride form with
-// 1024-4096 work-groups per class was slower still.
+// small 0.049 ms at 128K, 0.100 at 512K).  Smaller chunks on small sets
+// (the largest power of two down to 16K giving 2048 work-groups: 32K on
+// GPT-2-small, 16K on the 0.8M set) measured the same (0.047 ms, 0.015 ms).
+// A grid-stride form with 1024-4096 work-groups per class was slower still.
 constexpr int64_t kNormChunk = 131072;
 // A dispatch packet carries its grid size in work-items as a 32-bit value, so
 // launches over more chunks than fit are issued in pieces, each piece given
@@ -270,10 +273,18 @@ __device__ __forceinline__ void load_grad(const GT* G, float out[W]) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// norm pieces shared by pass 1, the flat norm and finalize
+// ---------------------------------------------------------------------------
 
-// ---------------------------------------------------------------------------
-// pass 1: unscale + non-finite flag + sum of squares
-// ---------------------------------------------------------------------------
+// Outputs of the finalize step (any pointer may be NULL).
+struct FinalizeArgs {
+    double max_norm;
+    float* norm_out;
+    float* coef_out;
+    float* found_inf_out;
+    Window* win;
+};
 
 struct NormArgs {
     const DevTensor* tensors;
@@ -299,7 +310,7 @@ __device__ __forceinline__ uint32_t wave_or(uint32_t x) {
     return x;
 }
 
-// Reduces (sum, flag) over a work-group of kBlock threads in a fixed order and
+// Reduces (sum, flag) over a work-group of NT threads in a fixed order and
 // returns the result in thread 0.
 template <int NT>
 __device__ __forceinline__ void block_reduce(double& s, uint32_t& f) {
@@ -334,6 +345,102 @@ __device__ __forceinline__ void norm_accum(float x, float inv, bool unscale, dou
     acc = fma(d, d, acc);  // u*u is exact in double
 }
 
+// One pass-1 chunk of `len` gradient elements from g, accumulated by a
+// work-group of kBlock threads into (acc, bad) of each thread.
+template <typename GT>
+__device__ __forceinline__ void norm_chunk(const GT* __restrict__ g, int64_t len, float inv, bool unscale, double& acc,
+                                           uint32_t& bad) {
+    int64_t done = 0;
+    if (aligned(g, sizeof(GT) * kVec)) {
+        const int64_t nvec = len / kVec;
+        int64_t i = threadIdx.x;
+        for (; i + (kNormUnroll - 1) * kBlock < nvec; i += kNormUnroll * kBlock) {
+            float x[kNormUnroll][kVec];
+#pragma unroll
+            for (int u = 0; u < kNormUnroll; ++u) load_grad<GT, kNtNormLoad, kVec>(g + (i + u * kBlock) * kVec, x[u]);
+#pragma unroll
+            for (int u = 0; u < kNormUnroll; ++u)
+#pragma unroll
+                for (int k = 0; k < kVec; ++k) norm_accum(x[u][k], inv, unscale, acc, bad);
+        }
+        for (; i < nvec; i += kBlock) {
+            float x[kVec];
+            load_grad<GT, kNtNormLoad, kVec>(g + i * kVec, x);
+#pragma unroll
+            for (int k = 0; k < kVec; ++k) norm_accum(x[k], inv, unscale, acc, bad);
+        }
+        done = nvec * kVec;
+    }
+    for (int64_t i = done + threadIdx.x; i < len; i += kBlock) norm_accum(GradIO<GT>::to_f32(g[i]), inv, unscale, acc, bad);
+}
+
+__device__ __forceinline__ float inv_scale_of(const float* scale) {
+    // grad_scaler.py:336-340: inv_scale = float(1 / double(scale))
+    return scale != nullptr ? static_cast<float>(1.0 / static_cast<double>(*scale)) : 1.0f;
+}
+
+// ---------------------------------------------------------------------------
+// finalize: total norm, clip coefficient, found_inf
+// ---------------------------------------------------------------------------
+
+// Sums the n partials in one work-group of kBlock threads, in an order that
+// depends on n only: thread j adds partials j, j + 512, j + 1024, ... in
+// turn (four loads in flight), then the fixed wave/LDS tree of block_reduce.
+// Thread 0 writes the norm, the clip coefficient and found_inf.  (Folding
+// this into pass 1's last work-group, through a device-scope counter and
+// release fence in every work-group, measured 2.3x slower for the norm pass
+// on the 8.2B set and 1.9x on GPT-2-small than this separate launch.)
+__device__ __forceinline__ void finalize_core(const Partial* partials, int64_t n, const FinalizeArgs& a) {
+    double s = 0.0;
+    uint32_t f = 0;
+    int64_t i = threadIdx.x;
+    for (; i + 3 * kBlock < n; i += 4 * kBlock) {
+        const Partial q0 = partials[i], q1 = partials[i + kBlock], q2 = partials[i + 2 * kBlock], q3 = partials[i + 3 * kBlock];
+        s += q0.sumsq;
+        s += q1.sumsq;
+        s += q2.sumsq;
+        s += q3.sumsq;
+        f |= q0.nonfinite | q1.nonfinite | q2.nonfinite | q3.nonfinite;
+    }
+    for (; i < n; i += kBlock) {
+        s += partials[i].sumsq;
+        f |= partials[i].nonfinite;
+    }
+    block_reduce<kBlock>(s, f);
+    if (threadIdx.x != 0) return;
+    // Norm of the stacked per-tensor norms = sqrt of the total sum of squares
+    // (clip_grad.py:96-108).  A sum beyond the fp32 range overflows to inf as
+    // torch's fp32 accumulation does.
+    float norm;
+    if (isnan(s)) norm = __builtin_nanf("");
+    else if (isinf(static_cast<float>(s))) norm = __builtin_inff();
+    else norm = static_cast<float>(sqrt(s));
+    if (a.norm_out) *a.norm_out = norm;
+    if (a.norm_out && a.win) {
+        a.win->norm_last = norm;
+        const float m = a.win->norm_max;
+        a.win->norm_max = (isnan(m) || isnan(norm)) ? __builtin_nanf("") : fmaxf(m, norm);
+    }
+    if (a.coef_out) {
+        // clip_grad.py:165-169 -> reciprocal(norm + 1e-6) * max_norm, clamp(max=1);
+        // NaN propagates through the clamp
+        const float d = norm + 1e-6f;
+        const float r = 1.0f / d;
+        float c = r * static_cast<float>(a.max_norm);
+        if (!isnan(c) && c > 1.0f) c = 1.0f;
+        *a.coef_out = c;
+    }
+    if (a.found_inf_out) *a.found_inf_out = f ? 1.0f : 0.0f;
+}
+
+__global__ void __launch_bounds__(kBlock) finalize_kernel(const Partial* partials, int64_t n, const FinalizeArgs a) {
+    finalize_core(partials, n, a);
+}
+
+// ---------------------------------------------------------------------------
+// pass 1: unscale + non-finite flag + sum of squares
+// ---------------------------------------------------------------------------
+
 template <typename GT>
 __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
     // work-group slot r (XCD-remapped) sums pass-1 chunk r of its class into
@@ -346,32 +453,7 @@ __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
     if (g != nullptr) {
         const int64_t numel = a.tensors[ck.tensor].numel;
         const int64_t start = static_cast<int64_t>(ck.index) * a.chunk_elems;
-        const int64_t len = min(a.chunk_elems, numel - start);
-        g += start;
-        const bool unscale = a.scale != nullptr;
-        const float inv = unscale ? static_cast<float>(1.0 / static_cast<double>(*a.scale)) : 1.0f;
-        int64_t done = 0;
-        if (aligned(g, sizeof(GT) * kVec)) {
-            const int64_t nvec = len / kVec;
-            int64_t i = threadIdx.x;
-            for (; i + (kNormUnroll - 1) * kBlock < nvec; i += kNormUnroll * kBlock) {
-                float x[kNormUnroll][kVec];
-#pragma unroll
-                for (int u = 0; u < kNormUnroll; ++u) load_grad<GT, kNtNormLoad, kVec>(g + (i + u * kBlock) * kVec, x[u]);
-#pragma unroll
-                for (int u = 0; u < kNormUnroll; ++u)
-#pragma unroll
-                    for (int k = 0; k < kVec; ++k) norm_accum(x[u][k], inv, unscale, acc, bad);
-            }
-            for (; i < nvec; i += kBlock) {
-                float x[kVec];
-                load_grad<GT, kNtNormLoad, kVec>(g + i * kVec, x);
-#pragma unroll
-                for (int k = 0; k < kVec; ++k) norm_accum(x[k], inv, unscale, acc, bad);
-            }
-            done = nvec * kVec;
-        }
-        for (int64_t i = done + threadIdx.x; i < len; i += kBlock) norm_accum(GradIO<GT>::to_f32(g[i]), inv, unscale, acc, bad);
+        norm_chunk<GT>(g + start, min(a.chunk_elems, numel - start), inv_scale_of(a.scale), a.scale != nullptr, acc, bad);
     }
     block_reduce<kBlock>(acc, bad);
     if (threadIdx.x == 0) {
@@ -384,66 +466,108 @@ __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// finalize: total norm, clip coefficient, found_inf
+// prologue: step counts and each tensor's constants for pass 2
 // ---------------------------------------------------------------------------
 
-__global__ void __launch_bounds__(kFinalizeBlock)
-    finalize_kernel(const Partial* partials, int64_t n, double max_norm, float* norm_out, float* coef_out,
-                    float* found_inf_out, Window* win) {
-    // each thread sums partials tid, tid + 1024, ... in that order (bounded
-    // by one CU's memory parallelism: 45 us for 125K partials, unrolled
-    // 8-deep the same; the Qwen3-8B set has 62,633 at 128K-element chunks)
-    double s = 0.0;
-    uint32_t f = 0;
-    for (int64_t i = threadIdx.x; i < n; i += kFinalizeBlock) {
-        s += partials[i].sumsq;
-        f |= partials[i].nonfinite;
-    }
-    block_reduce<kFinalizeBlock>(s, f);
-    if (threadIdx.x != 0) return;
-    // Norm of the stacked per-tensor norms = sqrt of the total sum of squares
-    // (clip_grad.py:96-108).  A sum beyond the fp32 range overflows to inf as
-    // torch's fp32 accumulation does.
-    float norm;
-    if (isnan(s)) norm = __builtin_nanf("");
-    else if (isinf(static_cast<float>(s))) norm = __builtin_inff();
-    else norm = static_cast<float>(sqrt(s));
-    if (norm_out) *norm_out = norm;
-    if (norm_out && win) {
-        win->norm_last = norm;
-        const float m = win->norm_max;
-        win->norm_max = (isnan(m) || isnan(norm)) ? __builtin_nanf("") : fmaxf(m, norm);
-    }
-    if (coef_out) {
-        // clip_grad.py:165-169 -> reciprocal(norm + 1e-6) * max_norm, clamp(max=1);
-        // NaN propagates through the clamp
-        const float d = norm + 1e-6f;
-        const float r = 1.0f / d;
-        float c = r * static_cast<float>(max_norm);
-        if (!isnan(c) && c > 1.0f) c = 1.0f;
-        *coef_out = c;
-    }
-    if (found_inf_out) *found_inf_out = f ? 1.0f : 0.0f;
+// The fp32 constants of one tensor's update this step, formed once per tensor
+// by the prologue and read by every pass-2 work-group of that tensor with
+// scalar loads.
+struct TensorConst {
+    float inv, coef, decay, w1, w1m1, b2, w2, bc2s, eps, nss;
+    uint32_t flags;  // kc* bits below
+    uint32_t pad;
+};
+static_assert(sizeof(TensorConst) == 48, "two scalar loads per record");
+constexpr uint32_t kcSkip = 1, kcUnscale = 2, kcClip = 4, kcDecay = 8, kcSmall = 16, kcMaximize = 32;
+
+struct PrologueArgs {
+    void* const* grads;
+    const DevTensor* tensors;
+    float* steps;
+    TensorConst* consts;
+    const double* bc;
+    int64_t bc_cap;
+    const float* scale;            // nullable
+    const float* coef;             // nullable
+    const float* found_inf;        // nullable
+    Window* win;                   // nullable
+    int* flags;                    // set to 1 when a tensor's bias corrections were computed here
+    const GroupConst* groups_dev;  // nullable: group records read from device memory at run time
+    int32_t n;
+    int32_t pad;
+    GroupConst groups[MGOPT_MAX_GROUPS];
+};
+
+__device__ __forceinline__ void count_window(Window* win, bool skip) {
+    if (win == nullptr) return;
+    if (skip) win->skipped += 1u;
+    else win->taken += 1u;
 }
 
-// ---------------------------------------------------------------------------
-// prologue: step counters
-// ---------------------------------------------------------------------------
-
-// adam.py:414 (step_t += 1) runs only when the step is taken: GradScaler skips
-// optimizer.step() on found_inf (grad_scaler.py:348-358); the fused path
-// subtracts found_inf back (adam.py:877-899).  Tensors without grad keep their
-// count (adam.py:153).
-__global__ void __launch_bounds__(kBlock)
-    prologue_kernel(const void* const* grads, float* steps, int32_t n, const float* found_inf, Window* win) {
-    const int32_t i = blockIdx.x * kBlock + threadIdx.x;
-    const bool skip = found_inf != nullptr && *found_inf != 0.0f;
-    if (win && i == 0) {
-        if (skip) win->skipped += 1u;
-        else win->taken += 1u;
+// (1 - beta1**t, (1 - beta2**t) ** 0.5) for step count t (adam.py:529-536).
+// Integer counts inside the host table read the host's values (Python's
+// float ** of the same expressions, so bit-identical to the CPU path); entry
+// 0 of a group's row holds the betas the row was built for.  Any other count
+// -- one written into the state in place, a non-integer count, a graph replay
+// beyond the table -- or betas other than the row's (a device record changed
+// between replays) is evaluated here in double with the same expressions; the
+// device pow can differ from the host's by an ulp of the double, which reaches
+// the fp32 constants only when it crosses one of their rounding boundaries.
+__device__ __forceinline__ void bias_corrections(const PrologueArgs& a, const GroupConst& G, int32_t group, float count,
+                                                 double& bc1, double& bc2s) {
+    const double t = static_cast<double>(count);
+    const double* row = a.bc + static_cast<int64_t>(group) * a.bc_cap * 2;
+    if (t >= 1.0 && t < static_cast<double>(a.bc_cap) && t == floor(t) && row[0] == G.beta1 && row[1] == G.beta2) {
+        const double* bc = row + static_cast<int64_t>(t) * 2;
+        bc1 = bc[0];
+        bc2s = bc[1];
+        return;
     }
-    if (i >= n || skip) return;
-    if (grads[i] != nullptr) steps[i] = steps[i] + 1.0f;
+    bc1 = 1.0 - pow(G.beta1, t);
+    bc2s = sqrt(1.0 - pow(G.beta2, t));
+    *a.flags = 1;
+}
+
+// One thread per tensor.  adam.py:414 (step_t += 1) runs only when the step is
+// taken: GradScaler skips optimizer.step() on found_inf
+// (grad_scaler.py:348-358); the fused path subtracts found_inf back
+// (adam.py:877-899).  Tensors without grad keep their count (adam.py:153).
+// The constants follow adam.py:416-547 and grad_scaler.py:336-340 in double,
+// each rounded to fp32 once, as torch's CPU path forms them.
+//
+// (Folding the step counts into pass 2 -- the last pass-2 work-group
+// advancing them after a device-scope counter -- measured 2.5x slower for pass
+// 2 on GPT-2-small and no faster on the 0.8M-parameter set.)
+__global__ void __launch_bounds__(kBlock) prologue_kernel(const PrologueArgs a) {
+    const bool skip = a.found_inf != nullptr && *a.found_inf != 0.0f;
+    if (blockIdx.x == 0 && threadIdx.x == 0) count_window(a.win, skip);
+    const int32_t i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= a.n) return;
+    TensorConst c{};
+    if (skip || a.grads[i] == nullptr) {
+        c.flags = kcSkip;
+        a.consts[i] = c;
+        return;
+    }
+    const float count = a.steps[i] + 1.0f;
+    a.steps[i] = count;
+    const int32_t group = a.tensors[i].group;
+    const GroupConst G = a.groups_dev != nullptr ? a.groups_dev[group] : a.groups[group];
+    double bc1, bc2s;
+    bias_corrections(a, G, group, count, bc1, bc2s);
+    c.inv = a.scale != nullptr ? static_cast<float>(1.0 / static_cast<double>(*a.scale)) : 1.0f;
+    c.coef = a.coef != nullptr ? *a.coef : 1.0f;
+    c.decay = static_cast<float>(1.0 - G.lr * G.wd);
+    c.w1 = static_cast<float>(1.0 - G.beta1);
+    c.w1m1 = c.w1 - 1.0f;
+    c.b2 = static_cast<float>(G.beta2);
+    c.w2 = static_cast<float>(1.0 - G.beta2);
+    c.bc2s = static_cast<float>(bc2s);
+    c.eps = static_cast<float>(G.eps);
+    c.nss = static_cast<float>(-(G.lr / bc1));
+    c.flags = (a.scale != nullptr ? kcUnscale : 0u) | (a.coef != nullptr ? kcClip : 0u) | (G.wd != 0.0 ? kcDecay : 0u) |
+              (fabsf(c.w1) < 0.5f ? kcSmall : 0u) | (G.maximize != 0 ? kcMaximize : 0u);
+    a.consts[i] = c;
 }
 
 // ---------------------------------------------------------------------------
@@ -454,17 +578,10 @@ struct AdamArgs {
     const DevTensor* tensors;
     const Chunk* chunks;
     void* const* grads;
-    const float* steps;
-    const double* bc;
-    int64_t bc_cap;
-    const float* scale;      // nullable
-    const float* coef;       // nullable
-    const float* found_inf;  // nullable
-    int* err;
+    const TensorConst* consts;
     int64_t chunk_elems;
     uint32_t chunk_begin;
     int32_t writeback;
-    GroupConst groups[MGOPT_MAX_GROUPS];
 };
 
 struct ElemConst {
@@ -589,38 +706,26 @@ struct Group {
     }
 };
 
+// The update of one pass-2 chunk of a tensor that has a gradient.
 template <typename GT, int LOWP>
-__global__ void __launch_bounds__(kAdamBlock) adamw_kernel(const AdamArgs a) {
-    const uint32_t cidx = a.chunk_begin + xcd_item<kXcdMapAdam>(blockIdx.x, gridDim.x);
-    const Chunk ck = a.chunks[cidx];
-    GT* __restrict__ g = static_cast<GT*>(a.grads[ck.tensor]);
-    if (g == nullptr) return;
-    if (a.found_inf != nullptr && *a.found_inf != 0.0f) return;  // skipped step
+__device__ __forceinline__ void adamw_chunk(const AdamArgs& a, const Chunk ck, GT* __restrict__ g, const TensorConst& k) {
     const DevTensor T = a.tensors[ck.tensor];
-    const GroupConst G = a.groups[T.group];
-    const int64_t t = static_cast<int64_t>(a.steps[ck.tensor]);
-    if (t < 1 || t >= a.bc_cap) {
-        if (threadIdx.x == 0) *a.err = 1;  // host table does not cover this step: leave the tensor untouched
-        return;
-    }
-    const double* bc = a.bc + (static_cast<int64_t>(T.group) * a.bc_cap + t) * 2;
-
     ElemConst c;
-    c.unscale = a.scale != nullptr;
-    c.inv = c.unscale ? static_cast<float>(1.0 / static_cast<double>(*a.scale)) : 1.0f;
-    c.clip = a.coef != nullptr;
-    c.coef = c.clip ? *a.coef : 1.0f;
-    c.maximize = G.maximize != 0;
-    c.do_decay = G.wd != 0.0;
-    c.decay = static_cast<float>(1.0 - G.lr * G.wd);
-    c.w1 = static_cast<float>(1.0 - G.beta1);
-    c.w1m1 = c.w1 - 1.0f;
-    c.small = fabsf(c.w1) < 0.5f;
-    c.b2 = static_cast<float>(G.beta2);
-    c.w2 = static_cast<float>(1.0 - G.beta2);
-    c.bc2s = static_cast<float>(bc[1]);
-    c.eps = static_cast<float>(G.eps);
-    c.nss = static_cast<float>(-(G.lr / bc[0]));
+    c.inv = k.inv;
+    c.coef = k.coef;
+    c.decay = k.decay;
+    c.w1 = k.w1;
+    c.w1m1 = k.w1m1;
+    c.b2 = k.b2;
+    c.w2 = k.w2;
+    c.bc2s = k.bc2s;
+    c.eps = k.eps;
+    c.nss = k.nss;
+    c.unscale = (k.flags & kcUnscale) != 0;
+    c.clip = (k.flags & kcClip) != 0;
+    c.do_decay = (k.flags & kcDecay) != 0;
+    c.small = (k.flags & kcSmall) != 0;
+    c.maximize = (k.flags & kcMaximize) != 0;
 
     const int64_t start = static_cast<int64_t>(ck.index) * a.chunk_elems;
     const int64_t len = min(a.chunk_elems, T.numel - start);
@@ -663,6 +768,15 @@ __global__ void __launch_bounds__(kAdamBlock) adamw_kernel(const AdamArgs a) {
         if constexpr (LOWP != MGOPT_NONE) LowpStore<LOWP>::store1(static_cast<uint16_t*>(L) + i, p);
         if (wb) g[i] = GradIO<GT>::from_f32(gc);
     }
+}
+
+template <typename GT, int LOWP>
+__global__ void __launch_bounds__(kAdamBlock) adamw_kernel(const AdamArgs a) {
+    const uint32_t cidx = a.chunk_begin + xcd_item<kXcdMapAdam>(blockIdx.x, gridDim.x);
+    const Chunk ck = a.chunks[cidx];
+    const TensorConst k = a.consts[ck.tensor];
+    if (k.flags & kcSkip) return;  // a skipped step, or no gradient this step
+    adamw_chunk<GT, LOWP>(a, ck, static_cast<GT*>(a.grads[ck.tensor]), k);
 }
 
 // ---------------------------------------------------------------------------
@@ -821,7 +935,8 @@ struct mgopt_plan {
     Chunk* d_norm_chunks = nullptr;  // pass 1: kNormChunk elements per chunk
     void** d_grads = nullptr;
     Partial* d_partials = nullptr;
-    int* d_err = nullptr;
+    int* d_flags = nullptr;          // set by the prologue when it computed bias corrections on the device
+    TensorConst* d_consts = nullptr;  // each tensor's constants for the coming pass 2 (written by the prologue)
     float* d_steps = nullptr;
     Window* d_window = nullptr;  // caller-owned, optional
     struct Class {
@@ -986,7 +1101,9 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
     hipError_t e;
     if ((e = hipMalloc(&P->d_tensors, sizeof(DevTensor) * n_tensors)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc tensors"));
     if ((e = hipMalloc(&P->d_grads, sizeof(void*) * n_tensors)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc grads"));
-    if ((e = hipMalloc(&P->d_err, sizeof(int))) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc err"));
+    if ((e = hipMalloc(&P->d_flags, sizeof(int))) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc flags"));
+    if ((e = hipMalloc(&P->d_consts, sizeof(TensorConst) * n_tensors)) != hipSuccess)
+        return cleanup(hip_fail(e, "hipMalloc consts"));
     if (P->n_chunks > 0) {
         if ((e = hipMalloc(&P->d_chunks, sizeof(Chunk) * P->n_chunks)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc chunks"));
         if ((e = hipMalloc(&P->d_norm_chunks, sizeof(Chunk) * norm_chunks.size())) != hipSuccess)
@@ -1001,7 +1118,7 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
     if ((e = hipMemcpy(P->d_tensors, host_t.data(), sizeof(DevTensor) * n_tensors, hipMemcpyHostToDevice)) != hipSuccess)
         return cleanup(hip_fail(e, "upload tensors"));
     if ((e = hipMemset(P->d_grads, 0, sizeof(void*) * n_tensors)) != hipSuccess) return cleanup(hip_fail(e, "clear grads"));
-    if ((e = hipMemset(P->d_err, 0, sizeof(int))) != hipSuccess) return cleanup(hip_fail(e, "clear err"));
+    if ((e = hipMemset(P->d_flags, 0, sizeof(int))) != hipSuccess) return cleanup(hip_fail(e, "clear flags"));
     for (int k = 0; k < kStagingSlots; ++k) {
         if ((e = hipHostMalloc(&P->staging[k], sizeof(void*) * n_tensors, hipHostMallocDefault)) != hipSuccess)
             return cleanup(hip_fail(e, "hipHostMalloc staging"));
@@ -1031,7 +1148,8 @@ MGOPT_API int mgopt_plan_destroy(mgopt_plan* P) {
     (void)hipFree(P->d_norm_chunks);
     (void)hipFree(P->d_grads);
     (void)hipFree(P->d_partials);
-    (void)hipFree(P->d_err);
+    (void)hipFree(P->d_flags);
+    (void)hipFree(P->d_consts);
     delete P;
     return 0;
 }
@@ -1072,8 +1190,8 @@ MGOPT_API int mgopt_grad_norm(mgopt_plan* P, const float* scale_dev, double max_
         }
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(kFinalizeBlock), 0, s, P->d_partials, P->n_partials, max_norm, norm_dev,
-                       coef_dev, found_inf_dev, P->d_window);
+    const FinalizeArgs fin{max_norm, norm_dev, coef_dev, found_inf_dev, P->d_window};
+    hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(kBlock), 0, s, P->d_partials, P->n_partials, fin);
     return launch_check("finalize_kernel");
 }
 
@@ -1081,41 +1199,35 @@ MGOPT_API int mgopt_adamw_step(mgopt_plan* P, const mgopt_group_hparams* groups,
                                const float* scale_dev, const float* coef_dev, const float* found_inf_dev, int32_t flags,
                                void* stream) {
     if (!P || !groups || !bc_dev) return fail(MGOPT_E_INVALID, "NULL argument");
+    const bool groups_on_device = (flags & MGOPT_GROUPS_ON_DEVICE) != 0;
     if (!P->has_state) return fail(MGOPT_E_INVALID, "grads-only plan: no optimizer state to update");
     if (!P->grads_uploaded) return fail(MGOPT_E_INVALID, "mgopt_plan_set_grads was not called");
     if (bc_cap < 2) return fail(MGOPT_E_INVALID, "bias-correction table too small");
     DeviceGuard guard(P->device);
     hipStream_t s = static_cast<hipStream_t>(stream);
 
-    hipLaunchKernelGGL(prologue_kernel, dim3((P->n_tensors + kBlock - 1) / kBlock), dim3(kBlock), 0, s,
-                       const_cast<const void* const*>(P->d_grads), P->d_steps, P->n_tensors, found_inf_dev, P->d_window);
+    PrologueArgs pa{};
+    pa.grads = P->d_grads;
+    pa.tensors = P->d_tensors;
+    pa.steps = P->d_steps;
+    pa.consts = P->d_consts;
+    pa.bc = bc_dev;
+    pa.bc_cap = bc_cap;
+    pa.scale = scale_dev;
+    pa.coef = coef_dev;
+    pa.found_inf = found_inf_dev;
+    pa.win = P->d_window;
+    pa.flags = P->d_flags;
+    pa.groups_dev = groups_on_device ? reinterpret_cast<const GroupConst*>(groups) : nullptr;
+    pa.n = P->n_tensors;
+    for (int gi = 0; gi < MGOPT_MAX_GROUPS && gi < P->n_groups && !groups_on_device; ++gi)
+        pa.groups[gi] = GroupConst{groups[gi].lr, groups[gi].weight_decay, groups[gi].beta1, groups[gi].beta2,
+                                   groups[gi].eps, groups[gi].maximize, 0};
+    hipLaunchKernelGGL(prologue_kernel, dim3((P->n_tensors + kBlock - 1) / kBlock), dim3(kBlock), 0, s, pa);
     if (int rc = launch_check("prologue_kernel")) return rc;
 
-    AdamArgs a;
-    a.tensors = P->d_tensors;
-    a.chunks = P->d_chunks;
-    a.grads = P->d_grads;
-    a.steps = P->d_steps;
-    a.bc = bc_dev;
-    a.bc_cap = bc_cap;
-    a.scale = scale_dev;
-    a.coef = coef_dev;
-    a.found_inf = found_inf_dev;
-    a.err = P->d_err;
-    a.chunk_elems = P->chunk_elems;
-    a.writeback = (flags & MGOPT_WRITEBACK_GRADS) ? 1 : 0;
-    for (int gi = 0; gi < MGOPT_MAX_GROUPS; ++gi) {
-        GroupConst gc{};
-        if (gi < P->n_groups) {
-            gc.lr = groups[gi].lr;
-            gc.wd = groups[gi].weight_decay;
-            gc.beta1 = groups[gi].beta1;
-            gc.beta2 = groups[gi].beta2;
-            gc.eps = groups[gi].eps;
-            gc.maximize = groups[gi].maximize;
-        }
-        a.groups[gi] = gc;
-    }
+    AdamArgs a{P->d_tensors, P->d_chunks, P->d_grads, P->d_consts, P->chunk_elems, 0,
+               (flags & MGOPT_WRITEBACK_GRADS) ? 1 : 0};
     for (const auto& c : P->classes) {
         a.chunk_begin = c.begin;
         int rc = 0;
@@ -1201,10 +1313,10 @@ MGOPT_API int mgopt_plan_set_window(mgopt_plan* P, void* window_dev) {
     return 0;
 }
 
-MGOPT_API int mgopt_plan_error_flag(mgopt_plan* P, int* out) {
+MGOPT_API int mgopt_plan_flags(mgopt_plan* P, int* out) {
     if (!P || !out) return fail(MGOPT_E_INVALID, "NULL argument");
     DeviceGuard guard(P->device);
-    HIP_TRY(hipMemcpy(out, P->d_err, sizeof(int), hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(out, P->d_flags, sizeof(int), hipMemcpyDeviceToHost));
     return 0;
 }
 

@@ -35,6 +35,8 @@ DEFAULT_CHUNK = 1024                # elements per pass-2 work-group (pass 1 has
                                     # 512 threads over 1024 elements retire fast and keep half the waves
                                     # of a CU streaming; 2-13 % faster than 16384 from 124M to 8.2B params
 BC_INITIAL_CAP = 1024               # first bias-correction table size (steps)
+CAPTURE_BC_CAP = 1 << 16            # fixed table size of a capturable engine (graph replays cannot grow it)
+HP_SLOTS = 4                        # pinned host buffers for device hyper-parameter uploads
 
 
 def _align(n: int) -> int:
@@ -43,8 +45,13 @@ def _align(n: int) -> int:
 
 def bias_correction_table(beta1: float, beta2: float, cap: int, start: int = 0) -> list[float]:
     """[bc1(t), sqrt(bc2)(t)] for t in start..cap-1, formed exactly as
-    torch/optim/adam.py:529-536 forms them from step = state["step"].item()."""
+    torch/optim/adam.py:529-536 forms them from step = state["step"].item();
+    entry t = 0 (never a step's count) holds [beta1, beta2], which the kernel
+    checks against the group's current betas before it uses the row."""
     out: list[float] = []
+    if start == 0:
+        out += [float(beta1), float(beta2)]
+        start = 1
     for t in range(start, cap):
         step = float(t)
         bias_correction1 = 1 - beta1**step
@@ -55,7 +62,8 @@ def bias_correction_table(beta1: float, beta2: float, cap: int, start: int = 0) 
 
 
 class _Engine:
-    def __init__(self, optimizer: torch.optim.Optimizer, master_weights: bool | None, chunk_elems: int | None):
+    def __init__(self, optimizer: torch.optim.Optimizer, master_weights: bool | None, chunk_elems: int | None,
+                 capturable: bool = False):
         # weak: the optimizer owns the engine, and a reference cycle would hold
         # the arenas (up to 100+ GB) until the cyclic collector happens to run
         self._opt_ref = weakref.ref(optimizer)
@@ -142,6 +150,11 @@ class _Engine:
         self.grad_dtype_bytes: bytes | None = None
         self.grad_source: list[torch.Tensor | None] | None = None
         self.grad_source_checked = False
+        # with a gradient arena: 1 where a parameter's gradient exists in the
+        # sense of torch's p.grad is not None (set when autograd accumulates
+        # into it, cleared by zero_grad(set_to_none=True)); None: every arena
+        # gradient counts
+        self.present: np.ndarray | None = None
         self.complete_keys: set[tuple[int, ...]] = set()   # id tuples of parameter lists equal to self.params
         self.t_bound = 0                     # upper bound of any step count reachable next step
         self.bc_cap = 0
@@ -152,6 +165,20 @@ class _Engine:
         self.hp = None                       # GroupHparams array passed to mgopt_adamw_step
         self.hp_key: list[tuple] | None = None
         self.hp_raw: list[tuple] | None = None
+        # capturable: the kernels read the group records from a fixed device
+        # buffer (refreshed from param_groups by asynchronous copies outside
+        # any capture), the bias-correction table has a fixed size, and once a
+        # step was captured the plan's device tables may not be replaced
+        self.capturable = capturable
+        self.captured = False
+        self.hp_dev: torch.Tensor | None = None
+        self.hp_dev_key: list[tuple] | None = None
+        if capturable:
+            with torch.cuda.device(dev):
+                self.hp_dev = torch.zeros(N.MAX_GROUPS * ctypes.sizeof(N.GroupHparams), dtype=torch.uint8, device=dev)
+            self.hp_slots = [torch.empty(self.hp_dev.numel(), dtype=torch.uint8, pin_memory=True) for _ in range(HP_SLOTS)]
+            self.hp_events: list[torch.cuda.Event | None] = [None] * HP_SLOTS
+            self.hp_slot = 0
         self.reset_iteration()
 
     @property
@@ -180,6 +207,12 @@ class _Engine:
             pass
 
     def _build_plan(self, grad_dtypes: tuple[int, ...]) -> None:
+        if self.captured:
+            raise RuntimeError("the gradient dtypes changed after a step of this optimizer was captured in a HIP "
+                               "graph; the graph reads this plan's device tables, so it cannot be rebuilt")
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("the optimizer's device plan does not exist yet: run one step outside graph capture "
+                               "before capturing")
         self.close()
         lib = N.lib()
         descs = (N.TensorDesc * len(self.params))()
@@ -228,6 +261,8 @@ class _Engine:
     def current_grads(self) -> list[torch.Tensor | None]:
         if self.grad_source is not None:
             return self.grad_source
+        if self.present is not None:
+            return [p.grad if k else None for p, k in zip(self.params, self.present)]
         return [p.grad for p in self.params]
 
     def prepare(self) -> None:
@@ -258,6 +293,13 @@ class _Engine:
         pptrs, gptrs, gdt, gflags = ps.gather()
         if pptrs != self.param_ptr_bytes:
             self._moved()
+        if self.present is not None and not self.present.all():
+            # arena gradients that torch would hold as None take no part
+            absent = self.present == 0
+            g = np.frombuffer(gptrs, np.int64).copy()
+            d = np.frombuffer(gdt, np.int8).copy()
+            g[absent], d[absent] = 0, -1
+            gptrs, gdt = g.tobytes(), d.tobytes()
         if gptrs == self.grad_ptr_bytes and gdt == self.grad_dtype_bytes and self.plan is not None:
             return
         flags = np.frombuffer(gflags, np.int8)
@@ -277,6 +319,10 @@ class _Engine:
         dtypes_t = tuple(prev[i] if c < 0 else int(c) for i, c in enumerate(codes))
         if self.plan is None or dtypes_t != self.plan_grad_dtypes:
             self._build_plan(dtypes_t)
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("the gradient tensors changed since the last step outside graph capture; a captured "
+                               "step reads gradients from fixed buffers (keep .grad tensors in place, for instance "
+                               "with use_grad_arena or zero_grad(set_to_none=False))")
         arr = ctypes.cast(ctypes.c_char_p(gptrs), ctypes.POINTER(ctypes.c_void_p))
         N.check(N.lib().mgopt_plan_set_grads(self.plan, arr, self._stream()),
                 "mgopt_plan_set_grads")
@@ -338,15 +384,25 @@ class _Engine:
 
     def _ensure_bc(self) -> None:
         """(Re)builds the bias-correction table when the reachable step bound
-        outgrows it or a group's betas changed."""
-        self.bc_src = self.hp_key
+        outgrows it or a group's betas changed.  A capturable engine's table
+        has a fixed size and is rewritten in place (a captured graph holds its
+        address); counts beyond it take the kernels' device evaluation."""
         keys = [(k[2], k[3]) for k in self.hp_key]
         need = self.t_bound + 2
-        if self.bc_table is not None and need <= self.bc_cap and keys == self.bc_keys:
+        if self.bc_table is not None and keys == self.bc_keys and (need <= self.bc_cap or self.capturable):
+            self.bc_src = self.hp_key
             return
-        cap = max(BC_INITIAL_CAP, self.bc_cap)
-        while cap < need:
-            cap *= 2
+        if torch.cuda.is_current_stream_capturing():
+            if self.bc_table is None:
+                raise RuntimeError("run one step outside graph capture before capturing")
+            return   # betas changed under capture: the kernels see a row built for other betas and evaluate on the device
+        self.bc_src = self.hp_key
+        if self.capturable:
+            cap = CAPTURE_BC_CAP
+        else:
+            cap = max(BC_INITIAL_CAP, self.bc_cap)
+            while cap < need:
+                cap *= 2
         # the host rows of groups whose betas are unchanged are extended, not
         # recomputed: a doubling at step t costs t new entries, not 2t
         old = dict(zip(self.bc_keys, self.bc_host)) if self.bc_table is not None else {}
@@ -356,7 +412,12 @@ class _Engine:
             row = list(row) if row is not None else []
             row.extend(bias_correction_table(b1, b2, cap, start=len(row) // 2))
             rows.append(row)
-        table = torch.tensor([x for row in rows for x in row], dtype=torch.float64).to(self.device)
+        host = torch.tensor([x for row in rows for x in row], dtype=torch.float64)
+        if self.capturable and self.bc_table is not None:
+            self.bc_table.copy_(host)
+            table = self.bc_table
+        else:
+            table = host.to(self.device)
         self.bc_table, self.bc_cap, self.bc_keys, self.bc_host = table, cap, keys, rows
 
     def sync_master(self) -> None:
@@ -370,9 +431,11 @@ class _Engine:
 
     def step(self, found_inf: torch.Tensor | None = None, grad_scale: torch.Tensor | None = None,
              writeback: bool = False) -> None:
-        groups = self.opt.param_groups
         self.prepare()
         if not self.master_synced:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("the master weights must be synced from the parameters outside graph capture "
+                                   "(run one step after loading or replacing parameters)")
             self.sync_master()
         scale = self.scale_src
         skip_src = None
@@ -384,31 +447,25 @@ class _Engine:
             if grad_scale is not None:
                 scale = grad_scale
             skip_src = found_inf
-        # the groups' values as stored: compared as they are, converted and
-        # checked only when one changed (a tensor lr is always re-read)
-        raw = [(g["lr"], g["weight_decay"], g["betas"], g["eps"], g.get("maximize", False), g.get("amsgrad", False))
-               for g in groups]
-        if any(isinstance(r[0], torch.Tensor) for r in raw) or raw != self.hp_raw:
-            key = []
-            for lr, wd, betas, eps, maximize, amsgrad in raw:
-                if amsgrad:
-                    raise NotImplementedError("amsgrad is not supported by mgopt AdamW")
-                key.append((float(lr.item() if isinstance(lr, torch.Tensor) else lr), float(wd),
-                            float(betas[0]), float(betas[1]), float(eps), bool(maximize)))
-            if key != self.hp_key:
-                # the hyperparameter block is rewritten only when a group changed
-                hp = (N.GroupHparams * len(groups))()
-                for d, (lr, wd, b1, b2, eps, maximize) in zip(hp, key):
-                    d.lr, d.weight_decay, d.beta1, d.beta2, d.eps, d.maximize = lr, wd, b1, b2, eps, int(maximize)
-                self.hp, self.hp_key = hp, key
-            self.hp_raw = None if any(isinstance(r[0], torch.Tensor) for r in raw) else raw
+        capturing = torch.cuda.is_current_stream_capturing()
+        self.read_hparams()
         self.t_bound += 1
         if self.t_bound + 2 > self.bc_cap or self.bc_src is not self.hp_key:
             self._ensure_bc()
         flags = N.WRITEBACK_GRADS if writeback else 0
+        groups_arg = self.hp
+        if self.capturable:
+            if capturing:
+                if self.hp_dev_key is None:
+                    raise RuntimeError("run one step outside graph capture before capturing")
+                self.captured = True
+            elif self.hp_dev_key != self.hp_key:
+                self.upload_hparams()
+            groups_arg = ctypes.c_void_p(self.hp_dev.data_ptr())
+            flags |= N.GROUPS_ON_DEVICE
         N.check(
             self._adamw_step(
-                self.plan, self.hp, self.bc_table.data_ptr(), self.bc_cap,
+                self.plan, groups_arg, self.bc_table.data_ptr(), self.bc_cap,
                 scale.data_ptr() if scale is not None else None,
                 self.coef.data_ptr() if self.clip_pending else None,
                 skip_src.data_ptr() if skip_src is not None else None,
@@ -417,6 +474,58 @@ class _Engine:
             "mgopt_adamw_step",
         )
         self.reset_iteration()
+
+    def read_hparams(self) -> None:
+        """Reads the groups' hyper-parameters into the record array passed to
+        the kernels.  The groups' values are compared as stored and converted
+        only when one changed (a tensor lr is always re-read)."""
+        groups = self.opt.param_groups
+        raw = [(g["lr"], g["weight_decay"], g["betas"], g["eps"], g.get("maximize", False), g.get("amsgrad", False))
+               for g in groups]
+        if not any(isinstance(r[0], torch.Tensor) for r in raw) and raw == self.hp_raw:
+            return
+        key = []
+        for lr, wd, betas, eps, maximize, amsgrad in raw:
+            if amsgrad:
+                raise NotImplementedError("amsgrad is not supported by mgopt AdamW")
+            key.append((float(lr.item() if isinstance(lr, torch.Tensor) else lr), float(wd),
+                        float(betas[0]), float(betas[1]), float(eps), bool(maximize)))
+        if key != self.hp_key:
+            # the record block is rewritten only when a group changed
+            hp = (N.GroupHparams * len(groups))()
+            for d, (lr, wd, b1, b2, eps, maximize) in zip(hp, key):
+                d.lr, d.weight_decay, d.beta1, d.beta2, d.eps, d.maximize = lr, wd, b1, b2, eps, int(maximize)
+            self.hp, self.hp_key = hp, key
+        self.hp_raw = None if any(isinstance(r[0], torch.Tensor) for r in raw) else raw
+
+    def upload_hparams(self) -> None:
+        """Copies the group records into the device buffer a capturable
+        engine's kernels read (asynchronous, from a pinned slot, on the
+        current stream)."""
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("hyper-parameters cannot be uploaded during graph capture")
+        k = self.hp_slot
+        if self.hp_events[k] is not None:
+            self.hp_events[k].synchronize()     # the slot may still feed an earlier copy
+        data = np.frombuffer(bytes(self.hp), np.uint8)
+        slot = self.hp_slots[k]
+        slot.numpy()[: data.size] = data
+        with torch.cuda.device(self.device):
+            self.hp_dev[: data.size].copy_(slot[: data.size], non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+        self.hp_events[k] = ev
+        self.hp_slot = (k + 1) % HP_SLOTS
+        self.hp_dev_key = self.hp_key
+
+    def refresh_hparams(self) -> None:
+        """Brings a capturable engine's device records up to date with
+        param_groups (before a graph replay)."""
+        self.read_hparams()
+        if self.capturable and self.hp_dev_key != self.hp_key:
+            if self.bc_table is not None and [(k[2], k[3]) for k in self.hp_key] != self.bc_keys:
+                self._ensure_bc()                # new betas: rewrite the table rows in place
+            self.upload_hparams()
 
     def window_metrics(self, reset: bool = True) -> dict:
         """Reads the log-window record (one device-to-host copy)."""
@@ -432,10 +541,12 @@ class _Engine:
             self.window.zero_()
         return out
 
-    def error_flag(self) -> int:
+    def device_bc_flag(self) -> int:
+        """1 once a step has computed bias corrections on the device (a step
+        count outside the host table), else 0.  Waits for the GPU."""
         out = ctypes.c_int(0)
         if self.plan is not None:
-            N.check(N.lib().mgopt_plan_error_flag(ctypes.c_void_p(self.plan), ctypes.byref(out)), "mgopt_plan_error_flag")
+            N.check(N.lib().mgopt_plan_flags(ctypes.c_void_p(self.plan), ctypes.byref(out)), "mgopt_plan_flags")
         return out.value
 
     def set_step_counts(self, counts: Sequence[float]) -> None:

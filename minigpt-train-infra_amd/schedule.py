@@ -45,9 +45,14 @@ def build_adamw_param_groups(model: torch.nn.Module, weight_decay: float) -> lis
 
 
 def set_optimizer_lr(optimizer: torch.optim.Optimizer, lr: float) -> None:
-    """Writes one learning rate into every group (src/minigpt/optim.py:67-71)."""
+    """Writes one learning rate into every group (src/minigpt/optim.py:67-71).
+    A capturable AdamW of this package also gets the value into the device
+    records a captured step reads (an asynchronous copy)."""
     for group in optimizer.param_groups:
         group["lr"] = lr
+    refresh = getattr(optimizer, "refresh_hparams", None)
+    if refresh is not None:
+        refresh()
 
 
 def cosine_lr(step: int, base_lr: float, min_lr: float, warmup_steps: int, max_steps: int) -> float:

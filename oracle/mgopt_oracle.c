@@ -164,6 +164,24 @@ ORC_API void orc_synth_fill(float* out, int64_t n, uint64_t seed, uint64_t strea
     for (int64_t i = 0; i < n; i++) out[i] = orc_synth_value(key, (uint64_t)i, k, tail_every, tail_mult);
 }
 
+/* The synthetic gradient of one tensor as the GPU holds it: elements
+ * [begin, end) of stream (seed, stream), stored in dtype (0 fp32, 1 fp16,
+ * 2 bf16; mgopt_synth_fill rounds to it) and read back as fp32. */
+static inline float synth_grad_value(uint64_t key, uint64_t i, double k, uint64_t tail_every, double tail_mult,
+                                     int dtype) {
+    float x = orc_synth_value(key, i, k, tail_every, tail_mult);
+    if (dtype == 1) return orc_f16_to_f32(orc_f32_to_f16(x));
+    if (dtype == 2) return orc_bf16_to_f32(orc_f32_to_bf16(x));
+    return x;
+}
+
+ORC_API void orc_synth_grad(float* out, int64_t begin, int64_t end, uint64_t seed, uint64_t stream, double k,
+                            uint64_t tail_every, double tail_mult, int dtype) {
+    uint64_t key = orc_synth_key(seed, stream);
+    for (int64_t i = begin; i < end; i++)
+        out[i - begin] = synth_grad_value(key, (uint64_t)i, k, tail_every, tail_mult, dtype);
+}
+
 /* ------------------------------------------------------------------------- */
 /* a5: GradScaler.unscale_                                                    */
 /* ------------------------------------------------------------------------- */
@@ -224,6 +242,32 @@ ORC_API void orc_grad_sumsq_acc(const void* data, int dtype, int64_t n, float in
     const uint16_t* h = (const uint16_t*)data;
     for (int64_t i = 0; i < n; i++) {
         float x = dtype == 0 ? f[i] : (dtype == 1 ? orc_f16_to_f32(h[i]) : orc_bf16_to_f32(h[i]));
+        if (!isfinite(x)) *found = 1.0f;
+        if (unscale && inv != 1.0f) x = x * inv;
+        double y = (double)x * (double)x;
+        double t = s + y;
+        if (!isfinite(t)) {
+            s = t;
+            c = 0.0;
+            continue;
+        }
+        if (fabs(s) >= fabs(y)) c += (s - t) + y;
+        else c += (y - t) + s;
+        s = t;
+    }
+    acc[0] = s;
+    acc[1] = c;
+}
+
+/* orc_grad_sumsq_acc over elements [begin, end) of a synthetic gradient
+ * (orc_synth_grad), generated on the fly instead of read from memory. */
+ORC_API void orc_synth_grad_sumsq_acc(int64_t begin, int64_t end, uint64_t seed, uint64_t stream, double k,
+                                      uint64_t tail_every, double tail_mult, int dtype, float inv, int unscale,
+                                      double* acc, float* found) {
+    uint64_t key = orc_synth_key(seed, stream);
+    double s = acc[0], c = acc[1];
+    for (int64_t i = begin; i < end; i++) {
+        float x = synth_grad_value(key, (uint64_t)i, k, tail_every, tail_mult, dtype);
         if (!isfinite(x)) *found = 1.0f;
         if (unscale && inv != 1.0f) x = x * inv;
         double y = (double)x * (double)x;

@@ -188,12 +188,16 @@ def grads_sumsq(grads, inv: float = 1.0, unscale: bool = False, threads: int = 1
         return acc, bool(found[0])
 
     with ThreadPoolExecutor(max_workers=max(1, threads)) as ex:
-        results = list(ex.map(run, jobs))
+        return _combine(list(ex.map(run, jobs)))
+
+
+def _combine(results) -> tuple[float, bool]:
+    """Folds per-piece (compensated sum, correction) pairs and non-finite
+    flags into one total, in the given (fixed) order."""
     acc = np.zeros(2, np.float64)
     found = False
     for a, f in results:
         found |= f
-        # fold each piece's (sum, correction) into the running compensated total
         for y in (a[0], a[1]):
             t = acc[0] + y
             if not np.isfinite(t):
@@ -202,6 +206,61 @@ def grads_sumsq(grads, inv: float = 1.0, unscale: bool = False, threads: int = 1
             acc[1] += (acc[0] - t) + y if abs(acc[0]) >= abs(y) else (y - t) + acc[0]
             acc[0] = t
     return float(acc[0] + acc[1]), found
+
+
+_GRAD_DTYPE = {"f32": 0, "f16": 1, "bf16": 2}
+
+
+def synth_grad(n: int, seed: int, stream: int, k: float, dtype: str = "f32", tail_every: int = 0,
+               tail_mult: float = 1.0, threads: int = 16, piece: int = 1 << 22) -> np.ndarray:
+    """The synthetic gradient the GPU generator writes into a `dtype` tensor
+    (mgopt_synth_fill), as fp32 values, generated in parallel pieces."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    L = lib()
+    L.orc_synth_grad.restype = None
+    L.orc_synth_grad.argtypes = [_F, ctypes.c_int64, ctypes.c_int64, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double,
+                                 ctypes.c_uint64, ctypes.c_double, ctypes.c_int]
+    out = np.empty(n, np.float32)
+    code = _GRAD_DTYPE[dtype]
+
+    def run(s):
+        e = min(n, s + piece)
+        L.orc_synth_grad(out[s:].ctypes.data_as(_F), s, e, seed, stream, k, tail_every, tail_mult, code)
+
+    with ThreadPoolExecutor(max_workers=max(1, threads)) as ex:
+        list(ex.map(run, range(0, n, piece)))
+    return out
+
+
+def synth_grads_sumsq(specs, inv: float = 1.0, unscale: bool = False, threads: int = 16,
+                      piece: int = 1 << 24) -> tuple[float, bool]:
+    """grads_sumsq over synthetic gradients generated on the fly: specs is a
+    list of (n, seed, stream, k, dtype, tail_every, tail_mult), one per tensor.
+    The pieces and their combination order are those grads_sumsq uses for
+    arrays of the same sizes, so the two give the same total."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    L = lib()
+    L.orc_synth_grad_sumsq_acc.restype = None
+    L.orc_synth_grad_sumsq_acc.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_uint64, ctypes.c_uint64,
+                                           ctypes.c_double, ctypes.c_uint64, ctypes.c_double, ctypes.c_int,
+                                           ctypes.c_float, ctypes.c_int, _D, _F]
+    jobs = []
+    for n, seed, stream, k, dt, tail_every, tail_mult in specs:
+        for s in range(0, n, piece):
+            jobs.append((s, min(n, s + piece), seed, stream, k, _GRAD_DTYPE[dt], tail_every, tail_mult))
+
+    def run(job):
+        s, e, seed, stream, k, code, tail_every, tail_mult = job
+        acc = np.zeros(2, np.float64)
+        found = np.zeros(1, np.float32)
+        L.orc_synth_grad_sumsq_acc(s, e, seed, stream, k, tail_every, tail_mult, code, inv, int(unscale),
+                                   acc.ctypes.data_as(_D), found.ctypes.data_as(_F))
+        return acc, bool(found[0])
+
+    with ThreadPoolExecutor(max_workers=max(1, threads)) as ex:
+        return _combine(list(ex.map(run, jobs)))
 
 
 def norm_from_sumsq(s: float) -> float:
@@ -225,6 +284,51 @@ def bias_corrections(beta1: float, beta2: float, step: float) -> tuple[float, fl
 def adamw(p, g, m, v, lr, beta1, beta2, eps, wd, step, maximize=False) -> None:
     """In-place AdamW update of one tensor (p, m, v float32, step = new count)."""
     lib().orc_adamw(_fp(p), _fp(g), _fp(m), _fp(v), p.size, lr, beta1, beta2, eps, wd, float(step), int(maximize))
+
+
+PIECE = 1 << 22          # elements per piece of the parallel element-wise helpers
+THREADS = 16             # threads of the parallel helpers (the GPU box's CPU share)
+
+
+def _pieces(n: int, fn, threads: int = THREADS, piece: int = PIECE) -> None:
+    """fn(s, e) over [0, n) in pieces of `piece` elements, in parallel threads
+    (the C calls release the GIL); serial when n fits one piece."""
+    if n <= piece:
+        fn(0, n)
+        return
+    from concurrent.futures import ThreadPoolExecutor
+
+    with ThreadPoolExecutor(max_workers=max(1, threads)) as ex:
+        list(ex.map(lambda s: fn(s, min(n, s + piece)), range(0, n, piece)))
+
+
+def adamw_parallel(p, g, m, v, lr, beta1, beta2, eps, wd, step, maximize=False, threads: int = THREADS,
+                   piece: int = PIECE) -> None:
+    """adamw() over pieces in parallel threads: the update is element-wise, so
+    the result is the same bits.  Each piece goes through this module's
+    adamw(), so a test that replaces it replaces every piece."""
+    fp, fg, fm, fv = (a.reshape(-1) for a in (p, g, m, v))
+    _pieces(fp.size, lambda s, e: adamw(fp[s:e], fg[s:e], fm[s:e], fv[s:e], lr, beta1, beta2, eps, wd, step, maximize),
+            threads, piece)
+
+
+def unscale_parallel(g: np.ndarray, inv: float) -> tuple[np.ndarray, bool]:
+    """unscale() in parallel pieces (same bits; found is the OR of the pieces')."""
+    out = np.empty_like(g)
+    flags = np.zeros(-(-g.size // PIECE) if g.size > PIECE else 1, np.float32)
+    L = lib()
+
+    def run(s, e):
+        k = s // PIECE if g.size > PIECE else 0
+        L.orc_unscale(_fp(g[s:e]), _fp(out[s:e]), e - s, inv, flags[k:].ctypes.data_as(_F))
+
+    _pieces(g.size, run)
+    return out, bool((flags != 0.0).any())
+
+
+def scale_parallel(g: np.ndarray, coef: float) -> None:
+    L = lib()
+    _pieces(g.size, lambda s, e: L.orc_scale(_fp(g[s:e]), e - s, coef))
 
 
 def adamw_mutant(p, g, m, v, lr, beta1, beta2, eps, wd, step, mutant: int) -> None:
@@ -282,7 +386,9 @@ class OracleRun:
         (used to compare the rest of the arithmetic against a reference whose
         norm differs).  totals: (sum of squares of the unscaled grads,
         non-finite flag) over every grad, computed elsewhere (grads_sumsq);
-        then grads need only hold the tensors of `subset`, the others None."""
+        then grads need only hold the tensors of `subset`, the others None.
+        A sum of squares of None leaves the norm unverified (out["norm"] is
+        None): the clip then uses norm_override, which must be given."""
         lrs = lr if isinstance(lr, list) else [lr] * len(self.hparams)
         found = False
         work = []
@@ -291,7 +397,7 @@ class OracleRun:
             if g is None:
                 work.append(None)
             elif self.scaler:
-                u, f = unscale(g, inv)
+                u, f = unscale_parallel(g, inv)
                 found |= f
                 work.append(u)
             else:
@@ -303,10 +409,14 @@ class OracleRun:
             sumsq = total_sumsq(present)
         norm = None
         if self.max_norm is not None and (present or totals is not None):
-            norm = norm_from_sumsq(sumsq)
+            if sumsq is None:
+                if norm_override is None:
+                    raise ValueError("an unverified norm needs norm_override")
+            else:
+                norm = norm_from_sumsq(sumsq)
             coef = clip_coef(norm if norm_override is None else norm_override, self.max_norm)
             for w in present:
-                scale_(w, coef)
+                scale_parallel(w, coef)
         skipped = bool(self.scaler) and found
         if not skipped:
             idx = range(len(self.p)) if subset is None else subset
@@ -315,8 +425,8 @@ class OracleRun:
                     continue
                 h = self.hparams[self.group_of[i]]
                 self.steps[i] += 1.0
-                adamw(self.p[i], work[i], self.m[i], self.v[i], lrs[self.group_of[i]], h["betas"][0], h["betas"][1],
-                      h["eps"], h["weight_decay"], self.steps[i], h.get("maximize", False))
+                adamw_parallel(self.p[i], work[i], self.m[i], self.v[i], lrs[self.group_of[i]], h["betas"][0],
+                               h["betas"][1], h["eps"], h["weight_decay"], self.steps[i], h.get("maximize", False))
         out = {"norm": norm, "found_inf": found, "skipped": skipped}
         if self.scaler:
             out["scale_before"] = self.scale

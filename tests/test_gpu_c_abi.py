@@ -3,9 +3,10 @@ ctypes declarations a caller outside this package would write, no package
 objects in the loop: a plan over three kernel classes (fp32 params with fp32
 and fp16 grads, bf16 params with an fp32 master), set_grads, grad_norm,
 adamw_step and scaler_update for several steps against the oracle bit for
-bit; the error returns a GPU process can see; and the kernel-side guard when
-the bias-correction table does not cover a step (forced from the host with a
-short table, so every kernel still exits normally)."""
+bit; the error returns a GPU process can see; step counts outside the
+bias-correction table (forced from the host with a short table, and a
+non-integer count written into the step array), which pass 2 evaluates on the
+device; and hyper-parameters read from device memory."""
 
 from __future__ import annotations
 
@@ -48,13 +49,12 @@ def _lib():
     lib.mgopt_plan_destroy.argtypes = [vp]
     lib.mgopt_plan_set_grads.argtypes = [vp, ctypes.POINTER(vp), vp]
     lib.mgopt_grad_norm.argtypes = [vp, vp, ctypes.c_double, vp, vp, vp, vp]
-    lib.mgopt_adamw_step.argtypes = [vp, ctypes.POINTER(GroupHparams), vp, ctypes.c_int64, vp, vp, vp, ctypes.c_int32,
-                                     vp]
+    lib.mgopt_adamw_step.argtypes = [vp, vp, vp, ctypes.c_int64, vp, vp, vp, ctypes.c_int32, vp]
     lib.mgopt_scaler_update.argtypes = [vp, vp, ctypes.POINTER(vp), ctypes.c_int32, ctypes.c_double, ctypes.c_double,
                                         ctypes.c_int32, vp]
     lib.mgopt_sync_master.argtypes = [vp, vp]
     lib.mgopt_plan_set_window.argtypes = [vp, vp]
-    lib.mgopt_plan_error_flag.argtypes = [vp, ctypes.POINTER(ctypes.c_int)]
+    lib.mgopt_plan_flags.argtypes = [vp, ctypes.POINTER(ctypes.c_int)]
     lib.mgopt_synth_fill.argtypes = [vp, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64, ctypes.c_uint64,
                                      ctypes.c_double, ctypes.c_uint64, ctypes.c_double, vp]
     lib.mgopt_last_error.restype = ctypes.c_char_p
@@ -76,10 +76,12 @@ def _fill(lib, t, seed, stream_id, sigma):
 
 
 def _bc_table(betas, cap):
-    """(1 - beta1**t, (1 - beta2**t) ** 0.5) for t < cap, as torch/optim/adam.py:529-536 forms them."""
+    """(1 - beta1**t, (1 - beta2**t) ** 0.5) for 1 <= t < cap, as torch/optim/adam.py:529-536
+    forms them, after the row's betas at t = 0."""
     out = []
     for b1, b2 in betas:
-        for t in range(cap):
+        out += [b1, b2]
+        for t in range(1, cap):
             out += [1 - b1 ** float(t), (1 - b2 ** float(t)) ** 0.5]
     return torch.tensor(out, dtype=torch.float64, device=DEV)
 
@@ -164,9 +166,9 @@ def test_three_kernel_classes_through_the_raw_abi():
                 assert np.array_equal(got.view(np.uint32), ref.ravel().view(np.uint32)), i
         bf = params[1].view(torch.int16).cpu().numpy().view(np.uint16)
         assert np.array_equal(bf, O.to_bf16(orc.p[1].ravel()))
-        err = ctypes.c_int(-1)
-        _ok(lib.mgopt_plan_error_flag(plan, ctypes.byref(err)), lib, "error_flag")
-        assert err.value == 0
+        flag = ctypes.c_int(-1)
+        _ok(lib.mgopt_plan_flags(plan, ctypes.byref(flag)), lib, "flags")
+        assert flag.value == 0
         log(f"[raw abi] 6 steps, one skipped; scale {float(scale)}, tracker {int(tracker)}")
     finally:
         lib.mgopt_plan_destroy(plan)
@@ -195,11 +197,7 @@ def test_error_returns_seen_by_a_gpu_caller():
         lib.mgopt_plan_destroy(plan)
 
 
-def test_short_bias_correction_table_leaves_the_tensor_untouched():
-    """Step 2 with a table covering only t < 2: pass 2 raises the plan's error
-    flag and leaves that tensor's parameter and moments as they were."""
-    lib = _lib()
-    n = 10000
+def _one_tensor_plan(lib, n, chunk=65536):
     p = torch.empty(n, dtype=torch.float32, device=DEV)
     _fill(lib, p, 1, 0, 0.02)
     g = torch.empty(n, dtype=torch.float32, device=DEV)
@@ -209,23 +207,80 @@ def test_short_bias_correction_table_leaves_the_tensor_untouched():
     d[0].param_dev, d[0].exp_avg_dev, d[0].exp_avg_sq_dev = p.data_ptr(), m.data_ptr(), v.data_ptr()
     d[0].numel, d[0].group, d[0].grad_dtype, d[0].lowp_dtype = n, 0, F32, NONE
     plan = ctypes.c_void_p()
-    _ok(lib.mgopt_plan_create(d, 1, 1, steps.data_ptr(), 65536, ctypes.byref(plan)), lib, "create")
+    _ok(lib.mgopt_plan_create(d, 1, 1, steps.data_ptr(), chunk, ctypes.byref(plan)), lib, "create")
+    return plan, p, g, m, v, steps
+
+
+def test_step_counts_outside_the_bias_correction_table():
+    """Steps 1-6 with a table covering only t < 3, then a count of 2.5 written
+    into the step array: every step updates the tensor, with the bias
+    corrections of the counts beyond the table evaluated on the device, and the
+    plan's flag reports it.  Checked against the oracle (host pow) at the fp32
+    tolerance, with the bit-exact fraction logged."""
+    lib = _lib()
+    n = 10000
+    plan, p, g, m, v, steps = _one_tensor_plan(lib, n)
     try:
         hp = (GroupHparams * 1)()
         hp[0].lr, hp[0].weight_decay, hp[0].beta1, hp[0].beta2, hp[0].eps = 1e-3, 0.1, 0.9, 0.95, 1e-8
-        bc = _bc_table([(0.9, 0.95)], 2)
+        bc = _bc_table([(0.9, 0.95)], 3)
+        torch.cuda.synchronize()
+        pr, mr, vr = p.cpu().numpy().copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
         _ok(lib.mgopt_plan_set_grads(plan, (ctypes.c_void_p * 1)(g.data_ptr()), _stream()), lib, "set_grads")
-        err = ctypes.c_int(-1)
-        for s in (1, 2):
+        flag = ctypes.c_int(-1)
+        count = 0.0
+        for s in range(1, 9):
+            if s == 7:
+                steps.fill_(2.5)      # a non-integer count written in place: the next step runs at 3.5
+                count = 2.5
             _fill(lib, g, 2, s, 1e-3)
-            before = [t.clone() for t in (p, m, v)]
-            _ok(lib.mgopt_adamw_step(plan, hp, bc.data_ptr(), 2, None, None, None, 0, _stream()), lib, "step")
             torch.cuda.synchronize()
-            _ok(lib.mgopt_plan_error_flag(plan, ctypes.byref(err)), lib, "error_flag")
-            changed = [not torch.equal(a, b) for a, b in zip(before, (p, m, v))]
-            if s == 1:
-                assert err.value == 0 and all(changed)
-            else:
-                assert err.value == 1 and not any(changed)
+            gh = g.cpu().numpy()
+            count += 1.0
+            O.adamw(pr, gh, mr, vr, 1e-3, 0.9, 0.95, 1e-8, 0.1, count)
+            _ok(lib.mgopt_adamw_step(plan, hp, bc.data_ptr(), 3, None, None, None, 0, _stream()), lib, "step")
+            torch.cuda.synchronize()
+            _ok(lib.mgopt_plan_flags(plan, ctypes.byref(flag)), lib, "flags")
+            assert flag.value == (1 if s >= 3 else 0), s
+            assert float(steps) == count
+            exact = []
+            for got, ref in ((p, pr), (m, mr), (v, vr)):
+                a = got.cpu().numpy()
+                assert np.max(np.abs(a.astype(np.float64) - ref) / np.maximum(np.abs(ref), 1e-30)) <= 1e-6, s
+                exact.append(float(np.mean(a.view(np.uint32) == ref.view(np.uint32))))
+            log(f"[short table] step {s} (count {count}): bit-exact fractions p/m/v {exact}")
     finally:
         lib.mgopt_plan_destroy(plan)
+
+
+def test_hyperparameters_from_device_memory_match_by_value():
+    """MGOPT_GROUPS_ON_DEVICE: the same step with the group record in device
+    memory (rewritten between steps, as a caller refreshes the learning rate
+    before a graph replay) gives the bits of the by-value record."""
+    lib = _lib()
+    n = 70000
+    a = _one_tensor_plan(lib, n, chunk=1024)
+    b = _one_tensor_plan(lib, n, chunk=1024)
+    try:
+        bc = _bc_table([(0.9, 0.95)], 16)
+        hp = (GroupHparams * 1)()
+        hp[0].weight_decay, hp[0].beta1, hp[0].beta2, hp[0].eps = 0.1, 0.9, 0.95, 1e-8
+        hp_dev = torch.zeros(6, dtype=torch.float64, device=DEV)   # 48 bytes: one mgopt_group_hparams
+        for plan, _, g, *_ in (a, b):
+            _ok(lib.mgopt_plan_set_grads(plan, (ctypes.c_void_p * 1)(g.data_ptr()), _stream()), lib, "set_grads")
+        for s in range(1, 6):
+            lr = 1e-3 * s
+            hp[0].lr = lr
+            hp_dev.copy_(torch.frombuffer(bytearray(bytes(hp)), dtype=torch.float64))
+            for _, _, g, *_ in (a, b):
+                _fill(lib, g, 3, s, 1e-3)
+            _ok(lib.mgopt_adamw_step(a[0], hp, bc.data_ptr(), 16, None, None, None, 0, _stream()), lib, "by value")
+            _ok(lib.mgopt_adamw_step(b[0], hp_dev.data_ptr(), bc.data_ptr(), 16, None, None, None, 2, _stream()), lib,
+                "on device")
+        torch.cuda.synchronize()
+        for x, y in zip(a[1:], b[1:]):
+            assert torch.equal(x.view(torch.int32), y.view(torch.int32))
+        assert float(a[5]) == float(b[5]) == 5.0
+    finally:
+        lib.mgopt_plan_destroy(a[0])
+        lib.mgopt_plan_destroy(b[0])

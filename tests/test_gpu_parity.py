@@ -126,7 +126,7 @@ def test_ragged_tensor_list_scaler_dynamics():
     assert pair.scaler._get_growth_tracker() == tracker
     steps = pair.opt._engine.steps.cpu().numpy()
     assert np.all(steps == 2000 - len(bad_steps))
-    assert pair.opt._engine.error_flag() == 0
+    assert pair.opt._engine.device_bc_flag() == 0
     log(f"[ragged] final scale {gpu_scales[-1]} tracker {tracker}")
 
 
@@ -150,3 +150,41 @@ def test_past_the_first_bias_correction_table_doubling():
     assert pair.opt._engine.bc_cap == 2048
     check_pair(pair, label="table_growth")
     assert all(float(pair.opt.state[p]["step"]) == 1100.0 for p in pair.params)
+
+
+def test_bf16_gradient_arena_bit_exact():
+    """bf16 params, bf16 gradients living in the optimizer's gradient arena
+    (AdamW.use_grad_arena: each .grad a view of one flat buffer with 256-byte
+    segment alignment), GradScaler with an inf at step 9, clip every step; 30
+    steps on a narrower GPT: every tensor bit-exact against the oracle."""
+    shapes = mg.paramsets.minigpt_shapes(vocab=4096, block=256, n_layer=2, n_embd=256)
+    log("case: bf16 gradient arena, 30 steps, inf at step 9")
+    pair = Pair(Case(shapes=shapes, param_dtype="bf16", grad_dtype="bf16", steps=30, sigma=1e-3, tail=(1000, 100.0),
+                     scaler=dict(init_scale=65536.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=7),
+                     inject={9: [(3, 17, float("inf"))]}, arena=True, fresh_grads=False))
+    views = [p.grad for p in pair.params]
+    pair.run()
+    assert all(p.grad is v for p, v in zip(pair.params, views))
+    assert all(v.untyped_storage().data_ptr() == pair.arena.untyped_storage().data_ptr() for v in views)
+    assert [s + 1 for s, o in enumerate(pair.outs) if o["skipped"]] == [9]
+    check_pair(pair, label="bf16_arena")
+
+
+def test_step_count_written_in_place_beyond_the_table():
+    """A step count written straight into the live state tensor
+    (state[p]["step"].fill_(...), which no Python hook sees) far beyond the
+    host's bias-correction table: the next steps still update every tensor,
+    with the bias corrections evaluated on the device, and the engine's flag
+    reports it.  Against the oracle at the fp32 tolerance, bit-exact fraction
+    logged."""
+    shapes = [("w", (64, 33)), ("b", (33,))]
+    pair = Pair(Case(shapes=shapes, steps=3, sigma=1e-2, max_norm=1.0))
+    pair.run(steps=3)
+    for i, p in enumerate(pair.params):
+        pair.opt.state[p]["step"].fill_(5000.0 + i)
+        pair.orc.steps[i] = 5000.0 + i
+    log("case: step counts 5000/5001 written in place, 3 more steps")
+    pair.run(steps=6, start=4)
+    assert pair.opt._engine.device_bc_flag() == 1
+    assert [float(pair.opt.state[p]["step"]) for p in pair.params] == [5003.0, 5004.0]
+    check_pair(pair, expect_exact=False, label="in_place_step", device_bc=1)

@@ -121,4 +121,4 @@ def test_random_configuration_against_the_oracle(seed):
             bits = p.detach().view(torch.int16).cpu().numpy().view(np.uint16).ravel()
             want = O.to_bf16(orc.p[k].ravel()) if c["pdt"] == "bf16" else O.to_f16(orc.p[k].ravel())
             assert np.array_equal(bits, want), (seed, k)
-    assert opt._engine.error_flag() == 0
+    assert opt._engine.device_bc_flag() == 0

@@ -724,7 +724,7 @@ def test_add_param_group_after_steps_matches_torch():
         assert maxrel(q.detach().cpu().numpy(), p.detach().numpy()) <= RTOL_STATE
         for k in ("exp_avg", "exp_avg_sq"):
             assert maxrel(opt.state[q][k].cpu().numpy(), topt.state[p][k].numpy()) <= RTOL_STATE
-    assert opt._engine.error_flag() == 0
+    assert opt._engine.device_bc_flag() == 0
 
 
 def test_add_param_group_keeps_bf16_masters_bit_exact():

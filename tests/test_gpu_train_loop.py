@@ -128,7 +128,7 @@ def test_training_loop_matches_torch_on_the_same_model():
     worst_param = _worst_param(ref_model, my_model)
     log(f"[train loop] worst rel: loss {worst_loss:.2e} norm {worst_norm:.2e} param {worst_param:.2e}")
     assert worst_loss <= 1e-6 and worst_norm <= 1e-6 and worst_param <= 1e-5
-    assert my_opt._engine.error_flag() == 0
+    assert my_opt._engine.device_bc_flag() == 0
 
 
 def test_accumulation_in_place_zeroing_and_a_torch_scheduler():
@@ -167,4 +167,90 @@ def test_accumulation_in_place_zeroing_and_a_torch_scheduler():
     worst_param = _worst_param(ref_model, my_model)
     log(f"[accumulation loop] worst rel: loss {worst_loss:.2e} norm {worst_norm:.2e} param {worst_param:.2e}")
     assert worst_loss <= 1e-6 and worst_norm <= 1e-6 and worst_param <= 1e-5
-    assert my_opt._engine.error_flag() == 0
+    assert my_opt._engine.device_bc_flag() == 0
+
+
+@pytest.mark.parametrize("set_to_none", [True, False])
+def test_grad_arena_accumulation_matches_torch(set_to_none):
+    """The gradient arena (AdamW.use_grad_arena: every .grad a view of one flat
+    buffer, zero_grad one fill) inside the accumulation loop of
+    train.py:465-481 -- 4 micro-batches, an inf at step 7 -- on a model with
+    MiniGPT's parameter structure plus a module the forward never reads,
+    against torch AdamW(fused=False, foreach=False) + GradScaler +
+    clip_grad_norm_ on a copy.  torch never gives the unused parameters a
+    gradient, so it never steps them and keeps no state for them: the arena
+    must do the same under both zero_grad modes.  Same bars as the loops
+    above."""
+    from tests._minigpt import MiniGPT, batches
+
+    torch.manual_seed(4)
+    ref_model = MiniGPT(unused_module=True).to(DEV)
+    my_model = copy.deepcopy(ref_model)
+    data = batches(24, seed=5)
+    kw = dict(lr=3e-3, betas=(0.9, 0.95), eps=1e-8)
+    ref_opt = torch.optim.AdamW(mg.build_adamw_param_groups(ref_model, 0.1), fused=False, foreach=False, **kw)
+    my_opt = mg.AdamW(mg.build_adamw_param_groups(my_model, 0.1), **kw)
+    arena = my_opt.use_grad_arena()
+    ref_scaler = torch.amp.GradScaler("cuda", init_scale=2.0**12, growth_interval=5)
+    my_scaler = mg.GradScaler("cuda", init_scale=2.0**12, growth_interval=5)
+    unused0 = [p.detach().clone() for p in my_model.unused.parameters()]
+
+    def loop(model, opt, scaler, clip):
+        losses, norms, scales = [], [], []
+        for s, (x, y) in enumerate(data, start=1):
+            mg.set_optimizer_lr(opt, mg.cosine_lr(s - 1, 3e-3, 3e-4, 3, len(data)))
+            opt.zero_grad(set_to_none=set_to_none)
+            total = 0.0
+            for xm, ym in zip(x.chunk(4), y.chunk(4)):
+                loss = nn.functional.cross_entropy(model(xm).flatten(0, 1), ym.flatten()) / 4
+                scaler.scale(loss).backward()
+                total = total + loss.detach()
+            if s == 7:
+                model.blocks[1].mlp.fc.weight.grad.view(-1)[3] = float("inf")
+            scaler.unscale_(opt)
+            norms.append(clip(model.parameters(), 1.0))
+            scaler.step(opt)
+            scaler.update()
+            losses.append(total)
+            scales.append(scaler.get_scale())
+        torch.cuda.synchronize()
+        return [float(v) for v in losses], [float(v) for v in norms], scales
+
+    log(f"case: gradient arena, set_to_none={set_to_none}, 4 micro-batches, unused module, 24 steps")
+    ref = loop(ref_model, ref_opt, ref_scaler, torch.nn.utils.clip_grad_norm_)
+    mine = loop(my_model, my_opt, my_scaler, mg.clip_grad_norm_)
+
+    # the arena stayed in place: every used parameter's gradient is still its view
+    used = [p for n, p in my_model.named_parameters() if not n.startswith("unused.")]
+    assert all(p.grad.untyped_storage().data_ptr() == arena.untyped_storage().data_ptr() for p in used)
+    # the unused module: never stepped, no state, as in torch
+    for p0, p, q in zip(unused0, my_model.unused.parameters(), ref_model.unused.parameters()):
+        assert torch.equal(p.detach(), p0) and torch.equal(q.detach(), p0)
+        assert not ref_opt.state.get(q) and not my_opt.state.get(p)
+        assert q.grad is None
+    # one entry per used parameter (named_parameters lists the tied head once)
+    assert len(my_opt.state_dict()["state"]) == len(ref_opt.state_dict()["state"]) == len(used)
+    assert mine[2] == ref[2]
+    assert mg.optimizer_completed_steps(my_opt) == mg.optimizer_completed_steps(ref_opt) == 23
+    worst_loss = max(abs(a - b) / abs(b) for a, b in zip(mine[0], ref[0]))
+    finite = [(a, b) for a, b in zip(mine[1], ref[1]) if math.isfinite(b)]
+    assert len(finite) == 23 and not math.isfinite(mine[1][6])
+    worst_norm = max(abs(a - b) / abs(b) for a, b in finite)
+    # The key third of each fused QKV bias (qkv_proj.bias[C:2C]) has an
+    # exactly zero gradient in exact arithmetic: softmax ignores a constant
+    # added to every score of a query.  Its computed gradient is rounding noise
+    # (~1e-10), which Adam divides by sqrt(v) + eps ~ eps, so each optimizer
+    # walks those elements by about lr * noise / eps per step along its own
+    # noise.  They are compared by that bound; every other element by the bar.
+    worst_param, worst_kbias = 0.0, 0.0
+    for (name, p), q in zip(ref_model.named_parameters(), my_model.parameters()):
+        a, b = p.detach().reshape(-1), q.detach().reshape(-1)
+        if name.endswith("attn.qkv_proj.bias"):
+            C = a.numel() // 3
+            worst_kbias = max(worst_kbias, (a[C:2 * C] - b[C:2 * C]).abs().max().item())
+            a, b = torch.cat([a[:C], a[2 * C:]]), torch.cat([b[:C], b[2 * C:]])
+        worst_param = max(worst_param, (a - b).abs().max().item() / max(a.abs().max().item(), 1e-30))
+    log(f"[arena set_to_none={set_to_none}] worst rel: loss {worst_loss:.2e} norm {worst_norm:.2e} param "
+        f"{worst_param:.2e}; key-bias abs diff {worst_kbias:.2e}")
+    assert worst_loss <= 1e-6 and worst_norm <= 1e-6 and worst_param <= 1e-5
+    assert worst_kbias <= len(data) * 3e-3 * 1e-1      # far below one full-size update per step

@@ -268,3 +268,48 @@ def test_synthetic_generator_statistics():
     t = O.synth(1_000_000, 9, 3, O.synth_k(1e-3), tail_every=1000, tail_mult=100.0)
     frac = np.mean(np.abs(t) > 1e-2)
     assert 0.0005 < frac < 0.0015
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_host_rebuilt_gradients_match_the_stored_path(dtype):
+    """The full-size tests rebuild gradients on the host from the generator
+    instead of copying them back: synth_grad equals the generator's values
+    rounded to the gradient dtype (what mgopt_synth_fill stores), and
+    synth_grads_sumsq equals grads_sumsq over those stored values, pieces and
+    combination order included -- with the heavy tail, unscaled and not."""
+    n, k = 3_000_001, O.synth_k(1e-2 * 1024.0)
+    stored = O.round_to(O.synth(n, 2, 77, k, 1000, 100.0), dtype)
+    rebuilt = O.synth_grad(n, 2, 77, k, dtype, 1000, 100.0, piece=1 << 20)
+    assert np.array_equal(rebuilt.view(np.uint32), stored.view(np.uint32))
+    raw = stored if dtype == "f32" else (O.to_f16(stored) if dtype == "f16" else O.to_bf16(stored))
+    for unscale in (False, True):
+        want = O.grads_sumsq([(raw, dtype)], inv=1 / 1024.0, unscale=unscale, piece=1 << 20)
+        got = O.synth_grads_sumsq([(n, 2, 77, k, dtype, 1000, 100.0)], inv=1 / 1024.0, unscale=unscale,
+                                  piece=1 << 20)
+        assert got == want
+
+
+def test_parallel_pieces_are_the_serial_arithmetic():
+    """adamw_parallel, unscale_parallel and scale_parallel split the
+    element-wise arithmetic into pieces run in threads: same bits as one
+    serial call, found_inf included (an inf in the last piece only)."""
+    rng = np.random.default_rng(7)
+    n = 3 * O.PIECE + 12345
+    g = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+    g[-3] = np.inf
+    u1, f1 = O.unscale(g, np.float32(1 / 512.0))
+    u2, f2 = O.unscale_parallel(g, np.float32(1 / 512.0))
+    assert f1 and f2 and np.array_equal(u1.view(np.uint32), u2.view(np.uint32))
+    g[-3] = 0.5
+    a, b = g.copy(), g.copy()
+    O.scale_(a, np.float32(0.37))
+    O.scale_parallel(b, np.float32(0.37))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    p = rng.standard_normal(n).astype(np.float32)
+    s1 = [p.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)]
+    s2 = [x.copy() for x in s1]
+    for step in (1, 2, 3):
+        O.adamw(s1[0], g, s1[1], s1[2], 1e-3, 0.9, 0.95, 1e-8, 0.1, step)
+        O.adamw_parallel(s2[0], g, s2[1], s2[2], 1e-3, 0.9, 0.95, 1e-8, 0.1, step)
+    for x, y in zip(s1, s2):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
