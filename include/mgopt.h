@@ -178,6 +178,20 @@ MGOPT_API int mgopt_plan_set_window(mgopt_plan* plan, void* window_dev);
  * counterpart. */
 MGOPT_API int mgopt_plan_flags(mgopt_plan* plan, int* out);
 
+/* The gradient L2 norm of one contiguous gradient buffer of n elements (a
+ * flat gradient arena), with the outputs, scaling and arithmetic of
+ * mgopt_grad_norm, and bit-identical to mgopt_grad_norm on a plan holding that
+ * buffer as its one tensor.  Allocates nothing: its
+ * partial sums live in a static 1 MiB device array that each GPU holds until
+ * the process ends, so n is at most 8,589,934,592 (65,536 chunks of 131,072
+ * elements; larger n returns MGOPT_E_LIMIT).  Runs on the current device.  Calls that overlap on
+ * one GPU share that array and race.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc). */
+MGOPT_API int mgopt_grad_norm_noalloc(const void* grads_dev, int32_t grad_dtype, int64_t n, const float* scale_dev,
+                                      double max_norm, float* norm_dev, float* coef_dev, float* found_inf_dev,
+                                      void* stream);
+
 /* Deterministic test data: dst[i] = synth(key(seed, stream_id), i) in dtype
  * (MGOPT_F32/F16/BF16).  No reference counterpart; used by tests and the
  * benchmark to create identical inputs on the GPU and in the CPU oracle. */

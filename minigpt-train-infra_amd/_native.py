@@ -31,6 +31,7 @@ EXPORTS = (
     "mgopt_sync_master",
     "mgopt_plan_set_window",
     "mgopt_plan_flags",
+    "mgopt_grad_norm_noalloc",
     "mgopt_synth_fill",
     "mgopt_last_error",
     "mgopt_version",
@@ -85,6 +86,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "mgopt_sync_master": (ctypes.c_int, [vp, vp]),
         "mgopt_plan_set_window": (ctypes.c_int, [vp, vp]),
         "mgopt_plan_flags": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_int)]),
+        "mgopt_grad_norm_noalloc": (ctypes.c_int, [vp, i32, i64, vp, dbl, vp, vp, vp, vp]),
         "mgopt_synth_fill": (ctypes.c_int, [vp, i32, i64, u64, u64, dbl, u64, dbl, vp]),
         "mgopt_last_error": (ctypes.c_char_p, []),
         "mgopt_version": (ctypes.c_char_p, []),

@@ -26,6 +26,7 @@
 #include <cmath>
 #include <cstdint>
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -462,6 +463,26 @@ __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
         p.nonfinite = bad;
         p.pad = 0;
         a.partials[a.partial_base + slot] = p;
+    }
+}
+
+// Pass 1 over one flat gradient buffer: work-group r sums elements
+// [r * kNormChunk, (r + 1) * kNormChunk) into partial r, the chunks and
+// partials a one-tensor plan has.
+template <typename GT>
+__global__ void __launch_bounds__(kBlock)
+    norm_flat_kernel(const GT* __restrict__ g, int64_t n, const float* scale, Partial* partials) {
+    double acc = 0.0;
+    uint32_t bad = 0;
+    const int64_t start = static_cast<int64_t>(blockIdx.x) * kNormChunk;
+    norm_chunk<GT>(g + start, min(kNormChunk, n - start), inv_scale_of(scale), scale != nullptr, acc, bad);
+    block_reduce<kBlock>(acc, bad);
+    if (threadIdx.x == 0) {
+        Partial p;
+        p.sumsq = acc;
+        p.nonfinite = bad;
+        p.pad = 0;
+        partials[blockIdx.x] = p;
     }
 }
 
@@ -1012,6 +1033,39 @@ int dtype_size(int32_t dt) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// allocation-free norm: partials in a static device array
+// ---------------------------------------------------------------------------
+
+// Partials of mgopt_grad_norm_noalloc, one per 131,072-element chunk: 1 MiB,
+// so one call covers at most 65,536 x 131,072 = 8,589,934,592 elements.  Each
+// GPU the library runs on holds its own copy until the process ends, and every
+// call on that GPU shares it (calls that overlap on one GPU race).  Every slot
+// a call reads is written by the same call, so nothing needs clearing.
+constexpr int64_t kScratchPartials = 65536;
+static __device__ __align__(256) Partial scratch[kScratchPartials];
+
+constexpr int kMaxDevices = 64;
+// The device address of `scratch` on each GPU, looked up once per GPU with
+// that GPU current.  Host code passes these addresses, never the symbol itself
+// (which names a host-side stand-in).
+std::atomic<Partial*> g_scratch_addr[kMaxDevices];
+
+int scratch_on_current_device(Partial** out) {
+    int dev = -1;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(MGOPT_E_LIMIT, "device index above 63");
+    Partial* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        void* addr = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)));
+        p = static_cast<Partial*>(addr);
+        g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1318,6 +1372,39 @@ MGOPT_API int mgopt_plan_flags(mgopt_plan* P, int* out) {
     DeviceGuard guard(P->device);
     HIP_TRY(hipMemcpy(out, P->d_flags, sizeof(int), hipMemcpyDeviceToHost));
     return 0;
+}
+
+MGOPT_API int mgopt_grad_norm_noalloc(const void* grads_dev, int32_t grad_dtype, int64_t n, const float* scale_dev,
+                                      double max_norm, float* norm_dev, float* coef_dev, float* found_inf_dev,
+                                      void* stream) {
+    if (n < 1 || grads_dev == nullptr) return fail(MGOPT_E_INVALID, "need n >= 1 and a gradient buffer");
+    const int64_t chunks = (n + kNormChunk - 1) / kNormChunk;
+    if (chunks > kScratchPartials)
+        return fail(MGOPT_E_LIMIT, "n = " + std::to_string(n) + " is above the allocation-free norm's maximum of " +
+                                       std::to_string(kScratchPartials * kNormChunk) + " elements");
+    Partial* part = nullptr;
+    if (int rc = scratch_on_current_device(&part)) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid(static_cast<unsigned>(chunks));
+    switch (grad_dtype) {
+        case MGOPT_F32:
+            hipLaunchKernelGGL(norm_flat_kernel<float>, grid, dim3(kBlock), 0, s, static_cast<const float*>(grads_dev), n,
+                               scale_dev, part);
+            break;
+        case MGOPT_F16:
+            hipLaunchKernelGGL(norm_flat_kernel<_Float16>, grid, dim3(kBlock), 0, s,
+                               static_cast<const _Float16*>(grads_dev), n, scale_dev, part);
+            break;
+        case MGOPT_BF16:
+            hipLaunchKernelGGL(norm_flat_kernel<Bf16>, grid, dim3(kBlock), 0, s, static_cast<const Bf16*>(grads_dev), n,
+                               scale_dev, part);
+            break;
+        default: return fail(MGOPT_E_INVALID, "bad grad dtype");
+    }
+    if (int rc = launch_check("norm_flat_kernel")) return rc;
+    const FinalizeArgs fin{max_norm, norm_dev, coef_dev, found_inf_dev, nullptr};
+    hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(kBlock), 0, s, part, chunks, fin);
+    return launch_check("finalize_kernel");
 }
 
 MGOPT_API int mgopt_synth_fill(void* dst, int32_t dtype, int64_t n, uint64_t seed, uint64_t stream_id, double k,
