@@ -541,6 +541,9 @@ class AdamW(torch.optim.Optimizer):
         if old is not None and (getattr(self, "_grad_arena", None) is not None or old.grad_source is not None):
             raise RuntimeError("add_param_group after use_grad_arena or set_grad_source is not supported: "
                                "those gradient buffers are laid out for the current parameters")
+        if old is not None and old.captured:
+            raise RuntimeError("add_param_group after a step of this optimizer was captured in a HIP graph is not "
+                               "supported: the graph reads the current state arenas, which a new group replaces")
         super().add_param_group(param_group)
         me = weakref.ref(self)
         for p in self.param_groups[-1]["params"]:

@@ -25,10 +25,10 @@ DEV = "cuda:0"
 SHAPES = [(64, 33), (1000,), (7,), (300, 5), (2, 131072)]
 
 
-def _setup(capturable: bool):
+def _setup(capturable: bool, dtype=torch.float32):
     params = []
     for i, s in enumerate(SHAPES):
-        p = torch.empty(s, dtype=torch.float32, device=DEV)
+        p = torch.empty(s, dtype=dtype, device=DEV)
         syn.fill_(p, syn.PARAM_SEED, syn.param_stream(i), 0.02)
         params.append(torch.nn.Parameter(p))
         params[-1].grad = torch.empty_like(p)          # fixed gradient buffers, rewritten in place
@@ -57,7 +57,9 @@ def _eager_step(params, opt, scaler):
 
 
 def _same(a, b):
-    return torch.equal(a.detach().reshape(-1).view(torch.int32), b.detach().reshape(-1).view(torch.int32))
+    x, y = a.detach().reshape(-1), b.detach().reshape(-1)
+    bits = torch.int32 if x.element_size() == 4 else torch.int16
+    return torch.equal(x.view(bits), y.view(bits))
 
 
 def _compare(pe, oe, se, pg, og, sg, norm_e, norm_g, label):
@@ -66,13 +68,16 @@ def _compare(pe, oe, se, pg, og, sg, norm_e, norm_g, label):
     assert se.get_scale() == sg.get_scale() and se._get_growth_tracker() == sg._get_growth_tracker(), label
     for a, b in zip(pe, pg):
         assert _same(a, b), label
-        for k in ("exp_avg", "exp_avg_sq", "step"):
+        for k in ("exp_avg", "exp_avg_sq", "step") + (("master_param",) if "master_param" in oe.state[a] else ()):
             assert _same(oe.state[a][k], og.state[b][k]), (label, k)
 
 
-def test_captured_step_replays_match_eager():
-    pe, oe, se = _setup(False)
-    pg, og, sg = _setup(True)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_captured_step_replays_match_eager(dtype):
+    """fp32 parameters, and bf16 parameters with fp32 masters (the bf16 copy
+    rewritten from the master by every replay)."""
+    pe, oe, se = _setup(False, dtype)
+    pg, og, sg = _setup(True, dtype)
     n_steps = 24
     lr_at = lambda s: mg.cosine_lr(s - 1, 3e-3, 3e-4, 4, n_steps)
     # two eager steps on both (the capturable one builds its plan, tables and device records)
@@ -112,7 +117,9 @@ def test_captured_step_replays_match_eager():
         norm_g2 = _eager_step(pg, og, sg)
         _compare(pe, oe, se, pg, og, sg, norm_e, norm_g2, f"eager step {s} after replays")
     assert og._engine.device_bc_flag() == 0 and og._engine.captured
-    log(f"[graph] 20 replays + 4 eager steps bit-exact against the eager twin; scale {sg.get_scale()}")
+    with pytest.raises(RuntimeError, match="captured"):
+        og.add_param_group({"params": [torch.nn.Parameter(torch.zeros(3, device=DEV))]})
+    log(f"[graph {dtype}] 20 replays + 4 eager steps bit-exact against the eager twin; scale {sg.get_scale()}")
 
 
 def test_capture_refuses_what_a_replay_cannot_honour():
