@@ -52,8 +52,23 @@ constexpr int kStagingSlots = 4;     // pinned host buffers for grad-pointer upl
 constexpr int kUnroll = 1;           // 4-element accesses in flight per thread before use
 constexpr bool kNtLoad = true;       // nontemporal loads of grad/param/exp_avg/exp_avg_sq
 constexpr bool kNtStore = true;      // nontemporal stores of param/exp_avg/exp_avg_sq
-constexpr int kNormUnroll = 2;       // pass-1 4-element accesses in flight per thread
-constexpr bool kNtNormLoad = true;   // nontemporal gradient loads in pass 1
+// Pass-1 accesses in flight per thread, and elements per access of 16-bit
+// gradients (fp32 gradients take 4, one 16-B access).  Unrolls of 4 and 8
+// and 16-B accesses of eight 16-bit values measured no faster on GPT-2-small
+// (0.053 ms), and 16-B accesses 7-8 % slower on the Qwen3-8B set's bf16
+// gradients (2.47-2.51 ms against 2.31).
+constexpr int kNormUnroll = 2;
+constexpr int kNormVec16 = 4;
+// Pass 2 reads the gradients pass 1 has just read.  When a plan's gradients
+// fit in the MI355X's 256 MB Infinity Cache (the memory-side cache in front
+// of HBM), pass 1 reads them with ordinary loads, which allocate there, and
+// pass 2's gradient reads hit it.  Measured on GPT-2-small (249 MB of fp16
+// gradients): pass 2 0.513 ms against 0.560 ms after nontemporal pass-1
+// loads, the whole step 0.573 against 0.614 ms.  Larger sets keep
+// nontemporal pass-1 loads: allocating made pass 1 up to 15 % slower on the
+// 2.6 GB and 16 GB gradient sets, with no gain in pass 2 beyond run-to-run
+// spread.  Nontemporal pass-2 gradient loads still hit the cache.
+constexpr int64_t kCachedGradBytes = int64_t(256) << 20;
 // pass 1 has its own chunk table of kNormChunk elements per chunk and
 // work-group, whatever the pass-2 chunk size: the finalize kernel then reads
 // one partial per 128K elements.  Pass 1 + finalize measured in one process
@@ -348,29 +363,30 @@ __device__ __forceinline__ void norm_accum(float x, float inv, bool unscale, dou
 
 // One pass-1 chunk of `len` gradient elements from g, accumulated by a
 // work-group of kBlock threads into (acc, bad) of each thread.
-template <typename GT>
+template <typename GT, bool NT>
 __device__ __forceinline__ void norm_chunk(const GT* __restrict__ g, int64_t len, float inv, bool unscale, double& acc,
                                            uint32_t& bad) {
+    constexpr int V = sizeof(GT) == 4 ? 4 : kNormVec16;
     int64_t done = 0;
-    if (aligned(g, sizeof(GT) * kVec)) {
-        const int64_t nvec = len / kVec;
+    if (aligned(g, sizeof(GT) * V)) {
+        const int64_t nvec = len / V;
         int64_t i = threadIdx.x;
         for (; i + (kNormUnroll - 1) * kBlock < nvec; i += kNormUnroll * kBlock) {
-            float x[kNormUnroll][kVec];
+            float x[kNormUnroll][V];
 #pragma unroll
-            for (int u = 0; u < kNormUnroll; ++u) load_grad<GT, kNtNormLoad, kVec>(g + (i + u * kBlock) * kVec, x[u]);
+            for (int u = 0; u < kNormUnroll; ++u) load_grad<GT, NT, V>(g + (i + u * kBlock) * V, x[u]);
 #pragma unroll
             for (int u = 0; u < kNormUnroll; ++u)
 #pragma unroll
-                for (int k = 0; k < kVec; ++k) norm_accum(x[u][k], inv, unscale, acc, bad);
+                for (int k = 0; k < V; ++k) norm_accum(x[u][k], inv, unscale, acc, bad);
         }
         for (; i < nvec; i += kBlock) {
-            float x[kVec];
-            load_grad<GT, kNtNormLoad, kVec>(g + i * kVec, x);
+            float x[V];
+            load_grad<GT, NT, V>(g + i * V, x);
 #pragma unroll
-            for (int k = 0; k < kVec; ++k) norm_accum(x[k], inv, unscale, acc, bad);
+            for (int k = 0; k < V; ++k) norm_accum(x[k], inv, unscale, acc, bad);
         }
-        done = nvec * kVec;
+        done = nvec * V;
     }
     for (int64_t i = done + threadIdx.x; i < len; i += kBlock) norm_accum(GradIO<GT>::to_f32(g[i]), inv, unscale, acc, bad);
 }
@@ -442,7 +458,8 @@ __global__ void __launch_bounds__(kBlock) finalize_kernel(const Partial* partial
 // pass 1: unscale + non-finite flag + sum of squares
 // ---------------------------------------------------------------------------
 
-template <typename GT>
+// NT: nontemporal gradient loads (sets larger than the Infinity Cache)
+template <typename GT, bool NT>
 __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
     // work-group slot r (XCD-remapped) sums pass-1 chunk r of its class into
     // partial r: the partials' order does not depend on the remapping
@@ -454,7 +471,8 @@ __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
     if (g != nullptr) {
         const int64_t numel = a.tensors[ck.tensor].numel;
         const int64_t start = static_cast<int64_t>(ck.index) * a.chunk_elems;
-        norm_chunk<GT>(g + start, min(a.chunk_elems, numel - start), inv_scale_of(a.scale), a.scale != nullptr, acc, bad);
+        norm_chunk<GT, NT>(g + start, min(a.chunk_elems, numel - start), inv_scale_of(a.scale), a.scale != nullptr, acc,
+                           bad);
     }
     block_reduce<kBlock>(acc, bad);
     if (threadIdx.x == 0) {
@@ -469,13 +487,13 @@ __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
 // Pass 1 over one flat gradient buffer: work-group r sums elements
 // [r * kNormChunk, (r + 1) * kNormChunk) into partial r, the chunks and
 // partials a one-tensor plan has.
-template <typename GT>
+template <typename GT, bool NT>
 __global__ void __launch_bounds__(kBlock)
     norm_flat_kernel(const GT* __restrict__ g, int64_t n, const float* scale, Partial* partials) {
     double acc = 0.0;
     uint32_t bad = 0;
     const int64_t start = static_cast<int64_t>(blockIdx.x) * kNormChunk;
-    norm_chunk<GT>(g + start, min(kNormChunk, n - start), inv_scale_of(scale), scale != nullptr, acc, bad);
+    norm_chunk<GT, NT>(g + start, min(kNormChunk, n - start), inv_scale_of(scale), scale != nullptr, acc, bad);
     block_reduce<kBlock>(acc, bad);
     if (threadIdx.x == 0) {
         Partial p;
@@ -970,6 +988,7 @@ struct mgopt_plan {
         uint32_t partial_base;  // first partial slot of the class
     };
     int64_t n_partials = 0;
+    int64_t grad_bytes = 0;  // all gradients of the plan, for pass 1's load policy
     std::vector<Class> classes;
     bool has_state = false;  // false: grads-only plan (norm and grad scaling only)
     std::vector<const void*> cached;
@@ -996,10 +1015,22 @@ int launch_norm(const mgopt_plan* P, const mgopt_plan::Class& c, const float* sc
         const uint32_t n = static_cast<uint32_t>(std::min<uint64_t>(c.norm_count - done, kMaxGroupsPerLaunch));
         NormArgs a{P->d_tensors, P->d_norm_chunks, P->d_grads, P->d_partials, scale, kNormChunk,
                    static_cast<uint32_t>(c.norm_begin + done), n, static_cast<uint32_t>(c.partial_base + done)};
-        hipLaunchKernelGGL(norm_kernel<GT>, dim3(n), dim3(kBlock), 0, s, a);
+        if (P->grad_bytes <= kCachedGradBytes)
+            hipLaunchKernelGGL((norm_kernel<GT, false>), dim3(n), dim3(kBlock), 0, s, a);
+        else
+            hipLaunchKernelGGL((norm_kernel<GT, true>), dim3(n), dim3(kBlock), 0, s, a);
         if (int rc = launch_check("norm_kernel")) return rc;
     }
     return 0;
+}
+
+template <typename GT>
+void launch_norm_flat(const void* grads, int64_t n, const float* scale, Partial* part, dim3 grid, hipStream_t s) {
+    const GT* g = static_cast<const GT*>(grads);
+    if (n * static_cast<int64_t>(sizeof(GT)) <= kCachedGradBytes)
+        hipLaunchKernelGGL((norm_flat_kernel<GT, false>), grid, dim3(kBlock), 0, s, g, n, scale, part);
+    else
+        hipLaunchKernelGGL((norm_flat_kernel<GT, true>), grid, dim3(kBlock), 0, s, g, n, scale, part);
 }
 
 template <typename GT, int LOWP>
@@ -1133,6 +1164,7 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
         c.count = static_cast<uint32_t>(chunks.size() - c.begin);
         c.norm_begin = static_cast<uint32_t>(norm_chunks.size());
         for (int32_t i : buckets[b]) {
+            P->grad_bytes += descs[i].numel * static_cast<int64_t>(dtype_size(descs[i].grad_dtype));
             const int64_t nch = (descs[i].numel + kNormChunk - 1) / kNormChunk;
             for (int64_t k = 0; k < nch; ++k) norm_chunks.push_back(Chunk{static_cast<uint32_t>(i), static_cast<uint32_t>(k)});
         }
@@ -1387,18 +1419,9 @@ MGOPT_API int mgopt_grad_norm_noalloc(const void* grads_dev, int32_t grad_dtype,
     hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<unsigned>(chunks));
     switch (grad_dtype) {
-        case MGOPT_F32:
-            hipLaunchKernelGGL(norm_flat_kernel<float>, grid, dim3(kBlock), 0, s, static_cast<const float*>(grads_dev), n,
-                               scale_dev, part);
-            break;
-        case MGOPT_F16:
-            hipLaunchKernelGGL(norm_flat_kernel<_Float16>, grid, dim3(kBlock), 0, s,
-                               static_cast<const _Float16*>(grads_dev), n, scale_dev, part);
-            break;
-        case MGOPT_BF16:
-            hipLaunchKernelGGL(norm_flat_kernel<Bf16>, grid, dim3(kBlock), 0, s, static_cast<const Bf16*>(grads_dev), n,
-                               scale_dev, part);
-            break;
+        case MGOPT_F32: launch_norm_flat<float>(grads_dev, n, scale_dev, part, grid, s); break;
+        case MGOPT_F16: launch_norm_flat<_Float16>(grads_dev, n, scale_dev, part, grid, s); break;
+        case MGOPT_BF16: launch_norm_flat<Bf16>(grads_dev, n, scale_dev, part, grid, s); break;
         default: return fail(MGOPT_E_INVALID, "bad grad dtype");
     }
     if (int rc = launch_check("norm_flat_kernel")) return rc;
