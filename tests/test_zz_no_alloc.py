@@ -4,7 +4,8 @@ same buffer as its one tensor.  Both sum the same 131,072-element chunks into
 partials and finalize them in the same fixed order, so norm, clip
 coefficient and found_inf must agree bit for bit.  Two calls in a row, the
 second over a smaller buffer, show that the static partials array keeps no
-state a later call depends on; sizes above its maximum are refused."""
+state a later call depends on; sizes above its maximum are refused.  Calls
+on either side of 256 MiB cover both of its load forms."""
 
 from __future__ import annotations
 
@@ -114,6 +115,26 @@ def test_noalloc_norm_matches_the_plan_norm(dtype):
         if use_scale:
             assert got[2] == (1.0 if inf_at is not None else 0.0)
         log(f"[noalloc {dtype}] call {call}: n {n}, norm {got[0]!r}, coef {got[1]!r}, found_inf {got[2]!r}")
+
+
+def test_noalloc_norm_on_both_sides_of_the_cache_size():
+    """Buffers of more than 256 MiB are read with nontemporal loads, smaller
+    ones with loads that leave them in the Infinity Cache: one call just above
+    that size and one just below, each against the plan norm (whose plan picks
+    its loads by the same rule) and, for the sum of squares, against the
+    oracle's compensated sum of the same elements."""
+    lib = _lib()
+    above, below = (256 << 20) // 4 + 1, (256 << 20) // 4 - 131072 - 7
+    buf = torch.empty(above, dtype=torch.float32, device=DEV)
+    for call, (n, seed) in enumerate([(above, 11), (below, 12)]):
+        log(f"case: noalloc fp32 n={n} ({'above' if n * 4 > (256 << 20) else 'below'} 256 MiB)")
+        _ok(lib.mgopt_synth_fill(buf.data_ptr(), F32, n, seed, 5, O.synth_k(1e-3), 0, 1.0, _stream()), lib, "fill")
+        got = _noalloc_norm(lib, buf, n, None, 1.0)
+        ref = _plan_norm(lib, buf[:n], None, 1.0)
+        assert _same(got, ref), (call, got, ref)
+        want = O.norm_from_sumsq(O.sumsq(buf[:n].cpu().numpy()))
+        assert got[0] == want, (call, got[0], want)
+        log(f"[noalloc cache sizes] n {n}: norm {got[0]!r} = oracle")
 
 
 def test_noalloc_norm_refuses_what_it_cannot_hold():
