@@ -104,6 +104,14 @@ MGOPT_API int mgopt_plan_destroy(mgopt_plan* plan);
 /* Number of pass-2 chunks of the plan (one work-group each). */
 MGOPT_API int64_t mgopt_plan_num_chunks(const mgopt_plan* plan);
 
+/* 1 when the plan runs a step as three kernels (a plan of at most 4,194,304
+ * elements, no empty tensor, MGOPT_FOLD not "0" in the environment at
+ * creation): pass 1 finalizes in its last work-group and pass 2 forms the
+ * step counts and constants itself; 0 for the five-kernel form (pass 1,
+ * finalize, prologue, pass 2, scaler); -1 for NULL.  Both forms give the same
+ * results.  No reference counterpart. */
+MGOPT_API int mgopt_plan_folded(const mgopt_plan* plan);
+
 /* Sets the gradient of every tensor for the coming step from a host array of
  * n_tensors device pointers (NULL = this tensor has no grad this step, as
  * p.grad is None is skipped at torch/optim/adam.py:153 and clip_grad.py:228).

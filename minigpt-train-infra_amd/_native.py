@@ -23,6 +23,7 @@ EXPORTS = (
     "mgopt_plan_create",
     "mgopt_plan_destroy",
     "mgopt_plan_num_chunks",
+    "mgopt_plan_folded",
     "mgopt_plan_set_grads",
     "mgopt_grad_norm",
     "mgopt_adamw_step",
@@ -78,6 +79,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "mgopt_plan_create": (ctypes.c_int, [ctypes.POINTER(TensorDesc), i32, i32, vp, i64, ctypes.POINTER(vp)]),
         "mgopt_plan_destroy": (ctypes.c_int, [vp]),
         "mgopt_plan_num_chunks": (i64, [vp]),
+        "mgopt_plan_folded": (ctypes.c_int, [vp]),
         "mgopt_plan_set_grads": (ctypes.c_int, [vp, ctypes.POINTER(vp), vp]),
         "mgopt_grad_norm": (ctypes.c_int, [vp, vp, dbl, vp, vp, vp, vp]),
         "mgopt_adamw_step": (ctypes.c_int, [vp, vp, vp, i64, vp, vp, vp, i32, vp]),

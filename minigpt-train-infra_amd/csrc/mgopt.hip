@@ -13,6 +13,10 @@
 //                              (+ bf16/fp16 model copy): unscale, clip, AdamW
 //   update   scaler_kernel     GradScaler scale/growth-tracker state machine
 //
+// Plans of at most 4M elements fold the finalize into pass 1 (the work-group
+// taking the last ticket runs it) and the prologue into pass 2
+// (adamw_fold_kernel): three kernels per step instead of five.
+//
 // Every scalar decision (skip, scale, coefficient, step count) stays on the
 // device, so the host never waits on the GPU inside a step.
 //
@@ -27,6 +31,7 @@
 #include <cstdint>
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -79,6 +84,16 @@ constexpr int64_t kCachedGradBytes = int64_t(256) << 20;
 // GPT-2-small, 16K on the 0.8M set) measured the same (0.047 ms, 0.015 ms).
 // A grid-stride form with 1024-4096 work-groups per class was slower still.
 constexpr int64_t kNormChunk = 131072;
+// Small plans (at most kFoldElems elements) run a step as three kernels
+// instead of five: pass 1 with the finalize in its last work-group, pass 2
+// with the prologue folded in, and the scaler update.  Dependent kernels wait
+// on each other, so on such plans the launches, not the bytes, set the step:
+// on the 0.8M-parameter set a captured step spans 26-29 us of GPU time against
+// 35-36 us in five kernels.  Their pass-1 chunks are shorter (4,096-16,384
+// measured the same).  MGOPT_FOLD=0 in the environment at plan creation keeps
+// the five-kernel form.
+constexpr int64_t kFoldElems = int64_t(1) << 22;
+constexpr int64_t kNormChunkFold = 16384;
 // A dispatch packet carries its grid size in work-items as a 32-bit value, so
 // launches over more chunks than fit are issued in pieces, each piece given
 // its first chunk (and first partial slot) as arguments.  8,388,607
@@ -312,6 +327,10 @@ struct NormArgs {
     uint32_t chunk_begin;
     uint32_t count;         // chunks of this launch's class
     uint32_t partial_base;  // first partial slot of this launch
+    // folded form only: the ticket counter, the plan's partial count and the finalize outputs
+    uint32_t* ticket;
+    uint32_t total;
+    FinalizeArgs fin;
 };
 
 __device__ __forceinline__ double wave_sum(double x) {
@@ -455,11 +474,34 @@ __global__ void __launch_bounds__(kBlock) finalize_kernel(const Partial* partial
 }
 
 // ---------------------------------------------------------------------------
+// tickets: the last work-group of a folded pass does the follow-on work
+// ---------------------------------------------------------------------------
+
+// Called by one thread of each work-group of a folded pass, after that
+// thread's last access that the follow-on work depends on (its partial's
+// atomic stores in pass 1, its read of a step count in pass 2).  The wait makes
+// every earlier access of the wave complete before the ticket is taken:
+// atomic stores are written through to the device's point of coherence, so no
+// L2 write-back is needed.  Returns the ticket, 0 .. total - 1.
+__device__ __forceinline__ uint32_t fetch_ticket(uint32_t* ticket) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // no earlier access moves below this point
+    __builtin_amdgcn_s_waitcnt(0);                         // every earlier access of this wave has completed
+    return __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// By the holder of the last ticket: every other ticket is taken, so the
+// counter starts the next launch at zero.
+__device__ __forceinline__ void reset_ticket(uint32_t* ticket) {
+    __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
 // pass 1: unscale + non-finite flag + sum of squares
 // ---------------------------------------------------------------------------
 
-// NT: nontemporal gradient loads (sets larger than the Infinity Cache)
-template <typename GT, bool NT>
+// NT: nontemporal gradient loads (sets larger than the Infinity Cache).
+// FOLD: small plans; the last work-group also runs the finalize.
+template <typename GT, bool NT, bool FOLD>
 __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
     // work-group slot r (XCD-remapped) sums pass-1 chunk r of its class into
     // partial r: the partials' order does not depend on the remapping
@@ -475,12 +517,28 @@ __global__ void __launch_bounds__(kBlock) norm_kernel(const NormArgs a) {
                            bad);
     }
     block_reduce<kBlock>(acc, bad);
-    if (threadIdx.x == 0) {
-        Partial p;
-        p.sumsq = acc;
-        p.nonfinite = bad;
-        p.pad = 0;
-        a.partials[a.partial_base + slot] = p;
+    if constexpr (!FOLD) {
+        if (threadIdx.x == 0) {
+            Partial p;
+            p.sumsq = acc;
+            p.nonfinite = bad;
+            p.pad = 0;
+            a.partials[a.partial_base + slot] = p;
+        }
+    } else {
+        __shared__ bool last;
+        if (threadIdx.x == 0) {
+            Partial* p = a.partials + a.partial_base + slot;
+            __hip_atomic_store(&p->sumsq, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&p->nonfinite, bad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = fetch_ticket(a.ticket) + 1 == a.total;
+            if (last) reset_ticket(a.ticket);
+        }
+        __syncthreads();
+        if (last) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // this XCD's cached lines of the partials are dropped
+            finalize_core(a.partials, a.total, a.fin);
+        }
     }
 }
 
@@ -567,29 +625,22 @@ __device__ __forceinline__ void bias_corrections(const PrologueArgs& a, const Gr
     *a.flags = 1;
 }
 
-// One thread per tensor.  adam.py:414 (step_t += 1) runs only when the step is
-// taken: GradScaler skips optimizer.step() on found_inf
-// (grad_scaler.py:348-358); the fused path subtracts found_inf back
-// (adam.py:877-899).  Tensors without grad keep their count (adam.py:153).
-// The constants follow adam.py:416-547 and grad_scaler.py:336-340 in double,
-// each rounded to fp32 once, as torch's CPU path forms them.
-//
-// (Folding the step counts into pass 2 -- the last pass-2 work-group
-// advancing them after a device-scope counter -- measured 2.5x slower for pass
-// 2 on GPT-2-small and no faster on the 0.8M-parameter set.)
-__global__ void __launch_bounds__(kBlock) prologue_kernel(const PrologueArgs a) {
-    const bool skip = a.found_inf != nullptr && *a.found_inf != 0.0f;
-    if (blockIdx.x == 0 && threadIdx.x == 0) count_window(a.win, skip);
-    const int32_t i = blockIdx.x * kBlock + threadIdx.x;
-    if (i >= a.n) return;
+// The constants of tensor i for this step (kcSkip when the step is skipped or
+// the tensor has no gradient; then `count` is its unchanged step count).
+// adam.py:414 (step_t += 1) runs only when the step is taken: GradScaler
+// skips optimizer.step() on found_inf (grad_scaler.py:348-358); the fused path
+// subtracts found_inf back (adam.py:877-899).  Tensors without grad keep their
+// count (adam.py:153).  The constants follow adam.py:416-547 and
+// grad_scaler.py:336-340 in double, each rounded to fp32 once, as torch's CPU
+// path forms them.
+__device__ __forceinline__ TensorConst tensor_const(const PrologueArgs& a, int32_t i, bool skip, float& count) {
     TensorConst c{};
     if (skip || a.grads[i] == nullptr) {
         c.flags = kcSkip;
-        a.consts[i] = c;
-        return;
+        count = a.steps[i];
+        return c;
     }
-    const float count = a.steps[i] + 1.0f;
-    a.steps[i] = count;
+    count = a.steps[i] + 1.0f;
     const int32_t group = a.tensors[i].group;
     const GroupConst G = a.groups_dev != nullptr ? a.groups_dev[group] : a.groups[group];
     double bc1, bc2s;
@@ -606,6 +657,21 @@ __global__ void __launch_bounds__(kBlock) prologue_kernel(const PrologueArgs a) 
     c.nss = static_cast<float>(-(G.lr / bc1));
     c.flags = (a.scale != nullptr ? kcUnscale : 0u) | (a.coef != nullptr ? kcClip : 0u) | (G.wd != 0.0 ? kcDecay : 0u) |
               (fabsf(c.w1) < 0.5f ? kcSmall : 0u) | (G.maximize != 0 ? kcMaximize : 0u);
+    return c;
+}
+
+// One thread per tensor: the step counts and the constants pass 2 reads.
+// (Large plans keep this kernel: advancing the counts from pass 2 through a
+// device-scope ticket in every work-group measured 2.5x slower for pass 2 on
+// GPT-2-small.  Small plans fold it into pass 2, adamw_fold_kernel.)
+__global__ void __launch_bounds__(kBlock) prologue_kernel(const PrologueArgs a) {
+    const bool skip = a.found_inf != nullptr && *a.found_inf != 0.0f;
+    if (blockIdx.x == 0 && threadIdx.x == 0) count_window(a.win, skip);
+    const int32_t i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= a.n) return;
+    float count;
+    const TensorConst c = tensor_const(a, i, skip, count);
+    if (!(c.flags & kcSkip)) a.steps[i] = count;
     a.consts[i] = c;
 }
 
@@ -745,6 +811,26 @@ struct Group {
     }
 };
 
+__device__ __forceinline__ ElemConst elem_const(const TensorConst& k) {
+    ElemConst c;
+    c.inv = k.inv;
+    c.coef = k.coef;
+    c.decay = k.decay;
+    c.w1 = k.w1;
+    c.w1m1 = k.w1m1;
+    c.b2 = k.b2;
+    c.w2 = k.w2;
+    c.bc2s = k.bc2s;
+    c.eps = k.eps;
+    c.nss = k.nss;
+    c.unscale = (k.flags & kcUnscale) != 0;
+    c.clip = (k.flags & kcClip) != 0;
+    c.do_decay = (k.flags & kcDecay) != 0;
+    c.small = (k.flags & kcSmall) != 0;
+    c.maximize = (k.flags & kcMaximize) != 0;
+    return c;
+}
+
 // The update of one pass-2 chunk of a tensor that has a gradient.
 template <typename GT, int LOWP>
 __device__ __forceinline__ void adamw_chunk(const AdamArgs& a, const Chunk ck, GT* __restrict__ g, const TensorConst& k) {
@@ -816,6 +902,72 @@ __global__ void __launch_bounds__(kAdamBlock) adamw_kernel(const AdamArgs a) {
     const TensorConst k = a.consts[ck.tensor];
     if (k.flags & kcSkip) return;  // a skipped step, or no gradient this step
     adamw_chunk<GT, LOWP>(a, ck, static_cast<GT*>(a.grads[ck.tensor]), k);
+}
+
+// Pass 2 of a small plan with the prologue folded in.  Every thread issues
+// the loads of its first element group, then thread 0 forms the tensor's
+// constants from the tensor's current step count (read, not written) and,
+// when the tensor has several chunks, takes one of the tensor's tickets; the
+// work-group of the tensor's last ticket (or of its only chunk) advances the
+// count once every work-group of the tensor has read it.
+template <typename GT, int LOWP>
+__global__ void __launch_bounds__(kAdamBlock)
+    adamw_fold_kernel(const AdamArgs a, const PrologueArgs pa, uint32_t* tickets) {
+    const Chunk ck = a.chunks[a.chunk_begin + blockIdx.x];
+    const bool skip = pa.found_inf != nullptr && *pa.found_inf != 0.0f;
+    const DevTensor T = a.tensors[ck.tensor];
+    GT* __restrict__ g = static_cast<GT*>(a.grads[ck.tensor]);
+    const int64_t start = static_cast<int64_t>(ck.index) * a.chunk_elems;
+    const int64_t len = min(a.chunk_elems, T.numel - start);
+    float* __restrict__ P = T.param + start;
+    float* __restrict__ M = T.m + start;
+    float* __restrict__ V = T.v + start;
+    void* L = nullptr;
+    if constexpr (LOWP != MGOPT_NONE) L = static_cast<uint16_t*>(T.lowp) + start;
+    if (g != nullptr) g += start;
+    const bool vec = g != nullptr && aligned(P, 16) && aligned(M, 16) && aligned(V, 16) &&
+                     aligned(g, sizeof(GT) * kVec) && (LOWP == MGOPT_NONE || aligned(L, 2 * kVec));
+    const int64_t nvec = vec ? len / kVec : 0;
+    const bool first = threadIdx.x < nvec;
+    Group<GT> q;
+    if (first) q.load(g, P, M, V, threadIdx.x * kVec);
+
+    __shared__ TensorConst kc;
+    const uint32_t nch = static_cast<uint32_t>((T.numel + a.chunk_elems - 1) / a.chunk_elems);
+    uint32_t t = 0;
+    float count = 0.0f;
+    if (threadIdx.x == 0) {
+        kc = tensor_const(pa, static_cast<int32_t>(ck.tensor), skip, count);
+        if (nch > 1) t = fetch_ticket(tickets + ck.tensor);
+    }
+    __syncthreads();
+    const TensorConst k = kc;
+    if (!(k.flags & kcSkip)) {
+        const ElemConst c = elem_const(k);
+        const bool wb = a.writeback != 0;
+        if (first) q.template finish<LOWP>(g, P, M, V, L, threadIdx.x * kVec, c, wb);
+        for (int64_t i = threadIdx.x + kAdamBlock; i < nvec; i += kAdamBlock) {
+            Group<GT> r;
+            r.load(g, P, M, V, i * kVec);
+            r.template finish<LOWP>(g, P, M, V, L, i * kVec, c, wb);
+        }
+        for (int64_t i = nvec * kVec + threadIdx.x; i < len; i += kAdamBlock) {
+            float p = P[i], m = M[i], v = V[i];
+            const float gc = adam_elem(GradIO<GT>::to_f32(g[i]), p, m, v, c);
+            P[i] = p;
+            M[i] = m;
+            V[i] = v;
+            if constexpr (LOWP != MGOPT_NONE) LowpStore<LOWP>::store1(static_cast<uint16_t*>(L) + i, p);
+            if (wb) g[i] = GradIO<GT>::from_f32(gc);
+        }
+    }
+    if (threadIdx.x != 0) return;
+    if (a.chunk_begin + blockIdx.x == 0) count_window(pa.win, skip);  // once per step, whatever the class launches
+    if (nch > 1) {
+        if (t + 1 != nch) return;
+        reset_ticket(tickets + ck.tensor);
+    }
+    if (!(k.flags & kcSkip)) pa.steps[ck.tensor] = count;
 }
 
 // ---------------------------------------------------------------------------
@@ -989,6 +1141,9 @@ struct mgopt_plan {
     };
     int64_t n_partials = 0;
     int64_t grad_bytes = 0;  // all gradients of the plan, for pass 1's load policy
+    int64_t norm_chunk = kNormChunk;  // elements per pass-1 chunk
+    bool fold = false;                // small plan: three kernels per step
+    uint32_t* d_tickets = nullptr;    // [0] pass 1, [1 + i] tensor i in pass 2 (folded form only)
     std::vector<Class> classes;
     bool has_state = false;  // false: grads-only plan (norm and grad scaling only)
     std::vector<const void*> cached;
@@ -1008,17 +1163,21 @@ int launch_check(const char* what) {
 }
 
 template <typename GT>
-int launch_norm(const mgopt_plan* P, const mgopt_plan::Class& c, const float* scale, hipStream_t s) {
+int launch_norm(const mgopt_plan* P, const mgopt_plan::Class& c, const float* scale, const FinalizeArgs& fin,
+                hipStream_t s) {
     // partial slot = partial_base + chunk position, so the pieces fill the
     // class's partials exactly as one launch would
     for (uint64_t done = 0; done < c.norm_count; done += kMaxGroupsPerLaunch) {
         const uint32_t n = static_cast<uint32_t>(std::min<uint64_t>(c.norm_count - done, kMaxGroupsPerLaunch));
-        NormArgs a{P->d_tensors, P->d_norm_chunks, P->d_grads, P->d_partials, scale, kNormChunk,
-                   static_cast<uint32_t>(c.norm_begin + done), n, static_cast<uint32_t>(c.partial_base + done)};
-        if (P->grad_bytes <= kCachedGradBytes)
-            hipLaunchKernelGGL((norm_kernel<GT, false>), dim3(n), dim3(kBlock), 0, s, a);
+        NormArgs a{P->d_tensors, P->d_norm_chunks, P->d_grads, P->d_partials, scale, P->norm_chunk,
+                   static_cast<uint32_t>(c.norm_begin + done), n, static_cast<uint32_t>(c.partial_base + done),
+                   P->d_tickets, static_cast<uint32_t>(P->n_partials), fin};
+        if (P->fold)
+            hipLaunchKernelGGL((norm_kernel<GT, false, true>), dim3(n), dim3(kBlock), 0, s, a);
+        else if (P->grad_bytes <= kCachedGradBytes)
+            hipLaunchKernelGGL((norm_kernel<GT, false, false>), dim3(n), dim3(kBlock), 0, s, a);
         else
-            hipLaunchKernelGGL((norm_kernel<GT, true>), dim3(n), dim3(kBlock), 0, s, a);
+            hipLaunchKernelGGL((norm_kernel<GT, true, false>), dim3(n), dim3(kBlock), 0, s, a);
         if (int rc = launch_check("norm_kernel")) return rc;
     }
     return 0;
@@ -1033,8 +1192,18 @@ void launch_norm_flat(const void* grads, int64_t n, const float* scale, Partial*
         hipLaunchKernelGGL((norm_flat_kernel<GT, true>), grid, dim3(kBlock), 0, s, g, n, scale, part);
 }
 
+// The extra arguments of a folded pass 2.
+struct FoldLaunch {
+    PrologueArgs pa;
+    uint32_t* tickets;  // one per tensor
+};
+
 template <typename GT, int LOWP>
-int launch_adamw(AdamArgs a, uint32_t count, hipStream_t s) {
+int launch_adamw(AdamArgs a, uint32_t count, const FoldLaunch* f, hipStream_t s) {
+    if (f != nullptr) {  // small plans: one piece
+        hipLaunchKernelGGL((adamw_fold_kernel<GT, LOWP>), dim3(count), dim3(kAdamBlock), 0, s, a, f->pa, f->tickets);
+        return launch_check("adamw_fold_kernel");
+    }
     const uint32_t begin = a.chunk_begin;
     for (uint64_t done = 0; done < count; done += kMaxGroupsPerLaunch) {
         const uint32_t n = static_cast<uint32_t>(std::min<uint64_t>(count - done, kMaxGroupsPerLaunch));
@@ -1046,11 +1215,11 @@ int launch_adamw(AdamArgs a, uint32_t count, hipStream_t s) {
 }
 
 template <typename GT>
-int launch_adamw_lowp(const AdamArgs& a, int32_t lowp, uint32_t count, hipStream_t s) {
+int launch_adamw_lowp(const AdamArgs& a, int32_t lowp, uint32_t count, const FoldLaunch* f, hipStream_t s) {
     switch (lowp) {
-        case MGOPT_NONE: return launch_adamw<GT, MGOPT_NONE>(a, count, s);
-        case MGOPT_BF16: return launch_adamw<GT, MGOPT_BF16>(a, count, s);
-        case MGOPT_F16: return launch_adamw<GT, MGOPT_F16>(a, count, s);
+        case MGOPT_NONE: return launch_adamw<GT, MGOPT_NONE>(a, count, f, s);
+        case MGOPT_BF16: return launch_adamw<GT, MGOPT_BF16>(a, count, f, s);
+        case MGOPT_F16: return launch_adamw<GT, MGOPT_F16>(a, count, f, s);
         default: return fail(MGOPT_E_INVALID, "unknown lowp dtype");
     }
 }
@@ -1145,6 +1314,17 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
 
     std::vector<Chunk> chunks, norm_chunks;
     mgopt_plan* P = new mgopt_plan();
+    // the folded pass 2 advances a tensor's count from one of its chunks, so a
+    // plan with an empty tensor keeps the prologue
+    int64_t total_elems = 0;
+    bool has_empty = false;
+    for (int32_t i = 0; i < n_tensors; ++i) {
+        total_elems += descs[i].numel;
+        has_empty |= descs[i].numel == 0;
+    }
+    const char* fold_env = std::getenv("MGOPT_FOLD");
+    P->fold = total_elems > 0 && total_elems <= kFoldElems && !has_empty && !(fold_env && std::strcmp(fold_env, "0") == 0);
+    P->norm_chunk = P->fold ? kNormChunkFold : kNormChunk;
     P->n_tensors = n_tensors;
     P->n_groups = n_groups;
     P->chunk_elems = chunk_elems;
@@ -1165,7 +1345,7 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
         c.norm_begin = static_cast<uint32_t>(norm_chunks.size());
         for (int32_t i : buckets[b]) {
             P->grad_bytes += descs[i].numel * static_cast<int64_t>(dtype_size(descs[i].grad_dtype));
-            const int64_t nch = (descs[i].numel + kNormChunk - 1) / kNormChunk;
+            const int64_t nch = (descs[i].numel + P->norm_chunk - 1) / P->norm_chunk;
             for (int64_t k = 0; k < nch; ++k) norm_chunks.push_back(Chunk{static_cast<uint32_t>(i), static_cast<uint32_t>(k)});
         }
         c.norm_count = static_cast<uint32_t>(norm_chunks.size() - c.norm_begin);
@@ -1205,6 +1385,11 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
         return cleanup(hip_fail(e, "upload tensors"));
     if ((e = hipMemset(P->d_grads, 0, sizeof(void*) * n_tensors)) != hipSuccess) return cleanup(hip_fail(e, "clear grads"));
     if ((e = hipMemset(P->d_flags, 0, sizeof(int))) != hipSuccess) return cleanup(hip_fail(e, "clear flags"));
+    if (P->fold) {
+        const size_t tb = sizeof(uint32_t) * (1 + static_cast<size_t>(n_tensors));
+        if ((e = hipMalloc(&P->d_tickets, tb)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc tickets"));
+        if ((e = hipMemset(P->d_tickets, 0, tb)) != hipSuccess) return cleanup(hip_fail(e, "clear tickets"));
+    }
     for (int k = 0; k < kStagingSlots; ++k) {
         if ((e = hipHostMalloc(&P->staging[k], sizeof(void*) * n_tensors, hipHostMallocDefault)) != hipSuccess)
             return cleanup(hip_fail(e, "hipHostMalloc staging"));
@@ -1236,11 +1421,14 @@ MGOPT_API int mgopt_plan_destroy(mgopt_plan* P) {
     (void)hipFree(P->d_partials);
     (void)hipFree(P->d_flags);
     (void)hipFree(P->d_consts);
+    (void)hipFree(P->d_tickets);
     delete P;
     return 0;
 }
 
 MGOPT_API int64_t mgopt_plan_num_chunks(const mgopt_plan* P) { return P ? P->n_chunks : -1; }
+
+MGOPT_API int mgopt_plan_folded(const mgopt_plan* P) { return P ? (P->fold ? 1 : 0) : -1; }
 
 MGOPT_API int mgopt_plan_set_grads(mgopt_plan* P, const void* const* grads_host, void* stream) {
     if (!P || !grads_host) return fail(MGOPT_E_INVALID, "NULL argument");
@@ -1266,17 +1454,18 @@ MGOPT_API int mgopt_grad_norm(mgopt_plan* P, const float* scale_dev, double max_
     if (!P->grads_uploaded) return fail(MGOPT_E_INVALID, "mgopt_plan_set_grads was not called");
     DeviceGuard guard(P->device);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    const FinalizeArgs fin{max_norm, norm_dev, coef_dev, found_inf_dev, P->d_window};
     for (const auto& c : P->classes) {
         int rc = 0;
         switch (c.grad_dtype) {
-            case MGOPT_F32: rc = launch_norm<float>(P, c, scale_dev, s); break;
-            case MGOPT_F16: rc = launch_norm<_Float16>(P, c, scale_dev, s); break;
-            case MGOPT_BF16: rc = launch_norm<Bf16>(P, c, scale_dev, s); break;
+            case MGOPT_F32: rc = launch_norm<float>(P, c, scale_dev, fin, s); break;
+            case MGOPT_F16: rc = launch_norm<_Float16>(P, c, scale_dev, fin, s); break;
+            case MGOPT_BF16: rc = launch_norm<Bf16>(P, c, scale_dev, fin, s); break;
             default: rc = fail(MGOPT_E_INVALID, "bad grad dtype");
         }
         if (rc) return rc;
     }
-    const FinalizeArgs fin{max_norm, norm_dev, coef_dev, found_inf_dev, P->d_window};
+    if (P->fold) return 0;  // the last pass-1 work-group ran the finalize
     hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(kBlock), 0, s, P->d_partials, P->n_partials, fin);
     return launch_check("finalize_kernel");
 }
@@ -1309,8 +1498,12 @@ MGOPT_API int mgopt_adamw_step(mgopt_plan* P, const mgopt_group_hparams* groups,
     for (int gi = 0; gi < MGOPT_MAX_GROUPS && gi < P->n_groups && !groups_on_device; ++gi)
         pa.groups[gi] = GroupConst{groups[gi].lr, groups[gi].weight_decay, groups[gi].beta1, groups[gi].beta2,
                                    groups[gi].eps, groups[gi].maximize, 0};
-    hipLaunchKernelGGL(prologue_kernel, dim3((P->n_tensors + kBlock - 1) / kBlock), dim3(kBlock), 0, s, pa);
-    if (int rc = launch_check("prologue_kernel")) return rc;
+    FoldLaunch fl{pa, P->d_tickets + 1};
+    const FoldLaunch* f = P->fold ? &fl : nullptr;
+    if (!P->fold) {
+        hipLaunchKernelGGL(prologue_kernel, dim3((P->n_tensors + kBlock - 1) / kBlock), dim3(kBlock), 0, s, pa);
+        if (int rc = launch_check("prologue_kernel")) return rc;
+    }
 
     AdamArgs a{P->d_tensors, P->d_chunks, P->d_grads, P->d_consts, P->chunk_elems, 0,
                (flags & MGOPT_WRITEBACK_GRADS) ? 1 : 0};
@@ -1318,9 +1511,9 @@ MGOPT_API int mgopt_adamw_step(mgopt_plan* P, const mgopt_group_hparams* groups,
         a.chunk_begin = c.begin;
         int rc = 0;
         switch (c.grad_dtype) {
-            case MGOPT_F32: rc = launch_adamw_lowp<float>(a, c.lowp_dtype, c.count, s); break;
-            case MGOPT_F16: rc = launch_adamw_lowp<_Float16>(a, c.lowp_dtype, c.count, s); break;
-            case MGOPT_BF16: rc = launch_adamw_lowp<Bf16>(a, c.lowp_dtype, c.count, s); break;
+            case MGOPT_F32: rc = launch_adamw_lowp<float>(a, c.lowp_dtype, c.count, f, s); break;
+            case MGOPT_F16: rc = launch_adamw_lowp<_Float16>(a, c.lowp_dtype, c.count, f, s); break;
+            case MGOPT_BF16: rc = launch_adamw_lowp<Bf16>(a, c.lowp_dtype, c.count, f, s); break;
             default: rc = fail(MGOPT_E_INVALID, "bad grad dtype");
         }
         if (rc) return rc;

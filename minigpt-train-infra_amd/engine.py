@@ -541,6 +541,11 @@ class _Engine:
             self.window.zero_()
         return out
 
+    def folded(self) -> bool:
+        """True when the plan runs a step as three kernels (a small plan: pass
+        1 finalizes in its last work-group, pass 2 forms the step counts)."""
+        return self.plan is not None and N.load_library().mgopt_plan_folded(ctypes.c_void_p(self.plan)) == 1
+
     def device_bc_flag(self) -> int:
         """1 once a step has computed bias corrections on the device (a step
         count outside the host table), else 0.  Waits for the GPU."""

@@ -134,6 +134,7 @@ def test_c_abi_rejects_bad_arguments_before_touching_the_gpu():
     assert lib.mgopt_synth_fill(None, native.F32, 0, 0, 0, 1.0, 0, 1.0, None) == 0
     assert lib.mgopt_grad_norm(None, None, 1.0, None, None, None, None) == 10001
     assert lib.mgopt_plan_num_chunks(None) == -1
+    assert lib.mgopt_plan_folded(None) == -1
 
 
 def test_product_has_no_cpu_path(mg):

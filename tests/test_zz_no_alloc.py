@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from pathlib import Path
 
 import pytest
@@ -60,11 +61,21 @@ def _stream():
 
 
 def _plan_norm(lib, g, scale, max_norm):
-    """mgopt_grad_norm over a grads-only plan with `g` as its one tensor."""
+    """mgopt_grad_norm over a grads-only plan with `g` as its one tensor, in
+    the five-kernel form (MGOPT_FOLD=0), whose pass 1 sums the same
+    131,072-element chunks as the allocation-free norm."""
     d = (TensorDesc * 1)()
     d[0].numel, d[0].group, d[0].grad_dtype, d[0].lowp_dtype = g.numel(), 0, CODES[g.dtype], NONE
     plan = ctypes.c_void_p()
-    _ok(lib.mgopt_plan_create(d, 1, 1, None, 65536, ctypes.byref(plan)), lib, "create")
+    saved = os.environ.get("MGOPT_FOLD")
+    os.environ["MGOPT_FOLD"] = "0"
+    try:
+        _ok(lib.mgopt_plan_create(d, 1, 1, None, 65536, ctypes.byref(plan)), lib, "create")
+    finally:
+        if saved is None:
+            del os.environ["MGOPT_FOLD"]
+        else:
+            os.environ["MGOPT_FOLD"] = saved
     out = [torch.full((), -1.0, dtype=torch.float32, device=DEV) for _ in range(3)]
     try:
         _ok(lib.mgopt_plan_set_grads(plan, (ctypes.c_void_p * 1)(g.data_ptr()), _stream()), lib, "set_grads")
