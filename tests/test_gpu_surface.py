@@ -12,7 +12,7 @@ import torch
 
 from oracle import oracle as O
 from tests._compare import RTOL_NORM, RTOL_STATE, exact_fraction, maxrel, rel
-from tests._gpu_harness import Case, Pair, check_pair, host_grad, log, mg, syn, to_f32
+from tests._gpu_harness import Case, Pair, check_pair, host_grad, mg, syn, to_f32
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
