@@ -123,7 +123,8 @@ MGOPT_API int mgopt_plan_set_grads(mgopt_plan* plan, const void* const* grads_ho
  *   torch._foreach_norm + vector_norm(stack)       (torch/nn/utils/clip_grad.py:96-108),
  *   the clip coefficient                           (clip_grad.py:165-169).
  * Reads every grad once (one pass-1 launch per gradient dtype, then one
- * finalize launch).  scale_dev: the GradScaler scale (fp32 scalar); when
+ * finalize launch; a small plan runs the finalize in pass 1's last
+ * work-group, see mgopt_plan_folded).  scale_dev: the GradScaler scale (fp32 scalar); when
  * non-NULL each grad element g becomes float(g) * float(1/double(scale))
  * before squaring, and found_inf_dev receives 1.0 if any *input* element is
  * non-finite, else 0.0.  coef_dev (when non-NULL) receives the clip
@@ -149,7 +150,8 @@ MGOPT_API int mgopt_grad_norm(mgopt_plan* plan, const float* scale_dev, double m
  * pow can differ from the host's by an ulp of the double), and raises the
  * plan's flag (mgopt_plan_flags).  A prologue launch (one thread per tensor)
  * advances the step counts and forms each tensor's fp32 constants; pass 2
- * then reads them once per work-group.
+ * then reads them once per work-group.  A small plan forms them inside
+ * pass 2 instead (mgopt_plan_folded), with the same results.
  * scale_dev (nullable): unscale as in mgopt_grad_norm.  coef_dev (nullable):
  * clip coefficient.  found_inf_dev (nullable): nonzero skips the whole step,
  * leaving params, moments and step counts untouched. */
