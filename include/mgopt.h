@@ -104,9 +104,9 @@ MGOPT_API int mgopt_plan_destroy(mgopt_plan* plan);
 /* Number of pass-2 chunks of the plan (one work-group each). */
 MGOPT_API int64_t mgopt_plan_num_chunks(const mgopt_plan* plan);
 
-/* 1 when the plan runs a step as three kernels (a plan of at most 4,194,304
- * elements, no empty tensor, MGOPT_FOLD not "0" in the environment at
- * creation): pass 1 finalizes in its last work-group and pass 2 forms the
+/* 1 when the plan runs a step as three kernels (a plan of at most 2,097,152
+ * elements, no empty tensor, no tensor of more than 256 pass-2 chunks,
+ * MGOPT_FOLD not "0" in the environment at creation): pass 1 finalizes in its last work-group and pass 2 forms the
  * step counts and constants itself; 0 for the five-kernel form (pass 1,
  * finalize, prologue, pass 2, scaler); -1 for NULL.  Both forms give the same
  * results.  No reference counterpart. */

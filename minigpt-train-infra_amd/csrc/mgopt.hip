@@ -13,7 +13,7 @@
 //                              (+ bf16/fp16 model copy): unscale, clip, AdamW
 //   update   scaler_kernel     GradScaler scale/growth-tracker state machine
 //
-// Plans of at most 4M elements fold the finalize into pass 1 (the work-group
+// Small plans (at most 2M elements) fold the finalize into pass 1 (the work-group
 // taking the last ticket runs it) and the prologue into pass 2
 // (adamw_fold_kernel): three kernels per step instead of five.
 //
@@ -84,18 +84,28 @@ constexpr int64_t kCachedGradBytes = int64_t(256) << 20;
 // GPT-2-small, 16K on the 0.8M set) measured the same (0.047 ms, 0.015 ms).
 // A grid-stride form with 1024-4096 work-groups per class was slower still.
 constexpr int64_t kNormChunk = 131072;
-// Small plans (at most kFoldElems elements) run a step as three kernels
-// instead of five: pass 1 with the finalize in its last work-group, pass 2
-// with the prologue folded in, and the scaler update.  Dependent kernels wait
-// on each other, so on such plans the launches, not the bytes, set the step:
-// on the 0.8M-parameter set a captured step spans 26-29 us of GPU time against
-// 35-36 us in five kernels.  Their pass-1 chunks are shorter (4,096-16,384
-// measured the same).  MGOPT_FOLD=0 in the environment at plan creation keeps
-// the five-kernel form.  (Folding only the finalize into a pass 1 of one round
-// of work-groups, GPT-2-small's 950, measured 0.567 ms per step both ways: the
-// ticket each work-group waits for costs what the saved launch gains.)
-constexpr int64_t kFoldElems = int64_t(1) << 22;
+// Small plans run a step as three kernels instead of five: pass 1 with the
+// finalize in its last work-group, pass 2 with the prologue folded in, and
+// the scaler update.  A plan qualifies with at most kFoldElems elements, no
+// empty tensor and no tensor of more than kFoldTensorChunks pass-2 chunks:
+// every chunk of a tensor takes a ticket from that tensor's counter, one
+// counter per 128-byte line, and the atomics on one line serialize.  Measured
+// per step on MI355X against the five-kernel form (eager / replayed graph,
+// us): the 0.8M-parameter MiniGPT set (52 tensors) 21.5 / 20.0 against
+// 26.2 / 21.3; 0.26M elements in one tensor 19.1 / 19.1 against 23.7 / 23.5;
+// 1M in 16 tensors 19.9 / 20.7 against 24.8 / 21.9; 2M in 16 tensors
+// 23.1 / 27.3 against 27.5 / 31.2; 4M in 16 tensors 38.7 / 43.0 against
+// 38.4 / 42.1; one tensor of 1M elements (1,024 chunks on one counter)
+// 24.3 / 29.0 against 25.3 / 24.7.  Their
+// pass-1 chunks are shorter (4,096-16,384 measured the same).  MGOPT_FOLD=0
+// in the environment at plan creation keeps the five-kernel form.  (Folding
+// only the finalize into a pass 1 of one round of work-groups, GPT-2-small's
+// 950, measured 0.567 ms per step both ways: the ticket each work-group waits
+// for costs what the saved launch gains.)
+constexpr int64_t kFoldElems = int64_t(1) << 21;
+constexpr int64_t kFoldTensorChunks = 256;
 constexpr int64_t kNormChunkFold = 16384;
+constexpr uint32_t kTicketStride = 32;  // uint32 counters per 128-byte line: one tensor's ticket per line
 // A dispatch packet carries its grid size in work-items as a 32-bit value, so
 // launches over more chunks than fit are issued in pieces, each piece given
 // its first chunk (and first partial slot) as arguments.  8,388,607
@@ -907,11 +917,12 @@ __global__ void __launch_bounds__(kAdamBlock) adamw_kernel(const AdamArgs a) {
 }
 
 // Pass 2 of a small plan with the prologue folded in.  Every thread issues
-// the loads of its first element group, then thread 0 forms the tensor's
-// constants from the tensor's current step count (read, not written) and,
-// when the tensor has several chunks, takes one of the tensor's tickets; the
-// work-group of the tensor's last ticket (or of its only chunk) advances the
-// count once every work-group of the tensor has read it.
+// the loads of its first element group while the first lane of the last wave
+// (no data in a 1,024-element chunk) forms the tensor's constants from the
+// tensor's current step count (read, not written) and, when the tensor has
+// several chunks, takes one of the tensor's tickets; the work-group of the
+// tensor's last ticket (or of its only chunk) advances the count once every
+// work-group of the tensor has read it.
 template <typename GT, int LOWP>
 __global__ void __launch_bounds__(kAdamBlock)
     adamw_fold_kernel(const AdamArgs a, const PrologueArgs pa, uint32_t* tickets) {
@@ -935,12 +946,13 @@ __global__ void __launch_bounds__(kAdamBlock)
     if (first) q.load(g, P, M, V, threadIdx.x * kVec);
 
     __shared__ TensorConst kc;
+    constexpr uint32_t kLead = kAdamBlock - 64;  // first lane of the last wave
     const uint32_t nch = static_cast<uint32_t>((T.numel + a.chunk_elems - 1) / a.chunk_elems);
     uint32_t t = 0;
     float count = 0.0f;
-    if (threadIdx.x == 0) {
+    if (threadIdx.x == kLead) {
         kc = tensor_const(pa, static_cast<int32_t>(ck.tensor), skip, count);
-        if (nch > 1) t = fetch_ticket(tickets + ck.tensor);
+        if (nch > 1) t = fetch_ticket(tickets + ck.tensor * kTicketStride);
     }
     __syncthreads();
     const TensorConst k = kc;
@@ -963,11 +975,11 @@ __global__ void __launch_bounds__(kAdamBlock)
             if (wb) g[i] = GradIO<GT>::from_f32(gc);
         }
     }
-    if (threadIdx.x != 0) return;
+    if (threadIdx.x != kLead) return;
     if (a.chunk_begin + blockIdx.x == 0) count_window(pa.win, skip);  // once per step, whatever the class launches
     if (nch > 1) {
         if (t + 1 != nch) return;
-        reset_ticket(tickets + ck.tensor);
+        reset_ticket(tickets + ck.tensor * kTicketStride);
     }
     if (!(k.flags & kcSkip)) pa.steps[ck.tensor] = count;
 }
@@ -1145,7 +1157,7 @@ struct mgopt_plan {
     int64_t grad_bytes = 0;  // all gradients of the plan, for pass 1's load policy
     int64_t norm_chunk = kNormChunk;  // elements per pass-1 chunk
     bool fold = false;                // small plan: three kernels per step
-    uint32_t* d_tickets = nullptr;    // [0] pass 1, [1 + i] tensor i in pass 2 (folded form only)
+    uint32_t* d_tickets = nullptr;    // [0] pass 1, [kTicketStride * (1 + i)] tensor i in pass 2 (folded form only)
     std::vector<Class> classes;
     bool has_state = false;  // false: grads-only plan (norm and grad scaling only)
     std::vector<const void*> cached;
@@ -1318,14 +1330,16 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
     mgopt_plan* P = new mgopt_plan();
     // the folded pass 2 advances a tensor's count from one of its chunks, so a
     // plan with an empty tensor keeps the prologue
-    int64_t total_elems = 0;
+    int64_t total_elems = 0, largest = 0;
     bool has_empty = false;
     for (int32_t i = 0; i < n_tensors; ++i) {
         total_elems += descs[i].numel;
+        largest = std::max(largest, descs[i].numel);
         has_empty |= descs[i].numel == 0;
     }
     const char* fold_env = std::getenv("MGOPT_FOLD");
-    P->fold = total_elems > 0 && total_elems <= kFoldElems && !has_empty && !(fold_env && std::strcmp(fold_env, "0") == 0);
+    P->fold = total_elems > 0 && total_elems <= kFoldElems && !has_empty &&
+              (largest + chunk_elems - 1) / chunk_elems <= kFoldTensorChunks && !(fold_env && std::strcmp(fold_env, "0") == 0);
     P->norm_chunk = P->fold ? kNormChunkFold : kNormChunk;
     P->n_tensors = n_tensors;
     P->n_groups = n_groups;
@@ -1388,7 +1402,7 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
     if ((e = hipMemset(P->d_grads, 0, sizeof(void*) * n_tensors)) != hipSuccess) return cleanup(hip_fail(e, "clear grads"));
     if ((e = hipMemset(P->d_flags, 0, sizeof(int))) != hipSuccess) return cleanup(hip_fail(e, "clear flags"));
     if (P->fold) {
-        const size_t tb = sizeof(uint32_t) * (1 + static_cast<size_t>(n_tensors));
+        const size_t tb = sizeof(uint32_t) * kTicketStride * (1 + static_cast<size_t>(n_tensors));
         if ((e = hipMalloc(&P->d_tickets, tb)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc tickets"));
         if ((e = hipMemset(P->d_tickets, 0, tb)) != hipSuccess) return cleanup(hip_fail(e, "clear tickets"));
     }
@@ -1500,7 +1514,7 @@ MGOPT_API int mgopt_adamw_step(mgopt_plan* P, const mgopt_group_hparams* groups,
     for (int gi = 0; gi < MGOPT_MAX_GROUPS && gi < P->n_groups && !groups_on_device; ++gi)
         pa.groups[gi] = GroupConst{groups[gi].lr, groups[gi].weight_decay, groups[gi].beta1, groups[gi].beta2,
                                    groups[gi].eps, groups[gi].maximize, 0};
-    FoldLaunch fl{pa, P->d_tickets + 1};
+    FoldLaunch fl{pa, P->d_tickets + kTicketStride};
     const FoldLaunch* f = P->fold ? &fl : nullptr;
     if (!P->fold) {
         hipLaunchKernelGGL(prologue_kernel, dim3((P->n_tensors + kBlock - 1) / kBlock), dim3(kBlock), 0, s, pa);

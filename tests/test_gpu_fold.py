@@ -1,9 +1,9 @@
 """The three-kernel step of small plans against the five-kernel step.
 
-A plan of at most 4,194,304 elements (and no empty tensor) runs pass 1 with
-the finalize in the work-group that takes its last ticket, and pass 2 with
-each tensor's step count and constants formed inside it, the tensor's last
-work-group advancing the count.  MGOPT_FOLD=0 in the environment when the
+A plan of at most 2,097,152 elements (no empty tensor, no tensor of more than
+256 pass-2 chunks) runs pass 1 with the finalize in the work-group that takes
+its last ticket, and pass 2 with each tensor's step count and constants
+formed inside it, the tensor's last work-group advancing the count.  MGOPT_FOLD=0 in the environment when the
 plan is created keeps the five-kernel form (pass 1, finalize, prologue, pass
 2, scaler).  The same training sequence through both forms must give the same
 norms, loss scales, step counts, parameters, moments, masters, low-precision
