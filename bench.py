@@ -10,6 +10,7 @@ Default workload: the Qwen3-8B-shaped parameter set (399 tensors,
 exp_avg_sq (131 GB resident), synthetic data.  Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+    python bench.py --workload uniform_262144x16 --no-cpu-baseline   # 16 fp32 tensors of 16,384 elements
     python bench.py --vs-torch [--workload NAME]   # torch's own GPU step beside this one
 """
 
@@ -73,11 +74,19 @@ def fill_tensors(tensors: list[torch.Tensor], seed: int, stream_of, sigma: float
             syn.fill_(t, seed, stream_of(i), sigma)
 
 
+def workload_spec(name: str) -> dict:
+    """Parameter and gradient dtypes of a workload (uniform_<n>x<k> sets: fp32)."""
+    if name in WORKLOADS:
+        return dict(WORKLOADS[name])
+    mg.paramsets.shapes_of(name)      # raises for an unknown name
+    return dict(param="f32", grad="f32")
+
+
 def build_workload(name: str, dev: torch.device, param_dtype: str | None = None):
-    spec = dict(WORKLOADS[name])
+    spec = workload_spec(name)
     if param_dtype is not None:
         spec["param"] = spec["grad"] = param_dtype
-    shapes = mg.paramsets.WORKLOADS[name]()
+    shapes = mg.paramsets.shapes_of(name)
     decay = [(n, s) for n, s in shapes if len(s) >= 2]
     nodecay = [(n, s) for n, s in shapes if len(s) < 2]
     ordered = decay + nodecay
@@ -96,7 +105,7 @@ def time_cpu_baseline(name: str, budget_params: int) -> dict:
     contiguous sample of the workload's tensors, extrapolated per parameter."""
     from oracle.torch_path import time_reference_step
 
-    shapes = mg.paramsets.WORKLOADS[name]()
+    shapes = mg.paramsets.shapes_of(name)
     # take tensors in model order (embeddings, then whole layers with their
     # norm weights) until the budget is reached, skipping any single tensor
     # that alone would overshoot it by more than half
@@ -247,12 +256,22 @@ def vs_torch(name: str, steps: int, warmup: int, dev: torch.device) -> dict:
     }
 
 
+def _workload_name(name: str) -> str:
+    try:
+        workload_spec(name)
+    except (KeyError, ValueError) as e:
+        raise argparse.ArgumentTypeError(str(e)) from None
+    return name
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=15)
-    ap.add_argument("--workload", default="qwen3_8b", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="qwen3_8b", type=_workload_name, metavar="NAME",
+                    help=f"one of {', '.join(sorted(WORKLOADS))}, or uniform_<params>x<tensors> (fp32 tensors "
+                         "of equal size, to see how the step scales)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-params", type=int, default=1_000_000_000)
     ap.add_argument("--vs-torch", action="store_true",

@@ -88,6 +88,29 @@ WORKLOADS = {
 }
 
 
+def uniform_shapes(n: int, k: int) -> list[tuple[str, Shape]]:
+    """k tensors of n // k elements each: a flat synthetic set for measuring
+    how the step scales with its size and tensor count.  Even indices are 2-D
+    (decay group), odd indices 1-D."""
+    if k < 1 or n < k:
+        raise ValueError(f"uniform set needs 1 <= k <= n, got n={n}, k={k}")
+    m = n // k
+    return [(f"u{i}", (1, m) if i % 2 == 0 else (m,)) for i in range(k)]
+
+
+def shapes_of(name: str) -> list[tuple[str, Shape]]:
+    """The parameter set of a named workload, or of 'uniform_<n>x<k>'
+    (uniform_shapes(n, k))."""
+    if name in WORKLOADS:
+        return WORKLOADS[name]()
+    parts = name.split("_", 1)
+    if len(parts) == 2 and parts[0] == "uniform":
+        n, _, k = parts[1].partition("x")
+        if n.isdigit() and k.isdigit():
+            return uniform_shapes(int(n), int(k))
+    raise KeyError(f"unknown workload {name!r}: one of {sorted(WORKLOADS)} or uniform_<params>x<tensors>")
+
+
 def numel(shape: Shape) -> int:
     n = 1
     for s in shape:

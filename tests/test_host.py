@@ -82,6 +82,13 @@ def test_workload_parameter_counts(mg):
     t, n = ps.count(shapes)
     assert t == 20000 and abs(n - 2.5e9) / 2.5e9 < 1e-3
     assert max(ps.numel(s) for _, s in shapes) <= 4 * 1024 * 1024 and min(ps.numel(s) for _, s in shapes) >= 1
+    # the flat synthetic sets used to measure how the step scales
+    shapes = ps.shapes_of("uniform_262144x16")
+    assert ps.count(shapes) == (16, 262_144) and sum(1 for _, s in shapes if len(s) >= 2) == 8
+    assert ps.shapes_of("minigpt_tiny_cpu") == ps.WORKLOADS["minigpt_tiny_cpu"]()
+    for bad in ("uniform_", "uniform_10x", "uniform_3x5", "uniform_0x0", "nope"):
+        with pytest.raises((KeyError, ValueError)):
+            ps.shapes_of(bad)
 
 
 def test_bias_correction_table_matches_oracle():
