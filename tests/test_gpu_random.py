@@ -11,6 +11,9 @@ state (params or masters, exp_avg, exp_avg_sq) bit-exact; the bf16 / fp16
 model copy equal to the round-to-nearest-even image of the master; norms
 within 1e-5 relative.
 
+Odd seeds create their plans with MGOPT_FOLD=0, so the five-kernel step is
+checked on small sets as well as the three-kernel step of small plans.
+
 MGOPT_RANDOM_CASES=N runs seeds 0..N-1 instead of the default 24.
 """
 
@@ -61,10 +64,13 @@ def _config(seed: int) -> dict:
 
 
 @pytest.mark.parametrize("seed", list(range(int(os.environ.get("MGOPT_RANDOM_CASES", "24")))))
-def test_random_configuration_against_the_oracle(seed):
+def test_random_configuration_against_the_oracle(seed, monkeypatch):
     c = _config(seed)
+    five = seed % 2 == 1
+    if five:
+        monkeypatch.setenv("MGOPT_FOLD", "0")
     log(f"case: seed {seed} {c['pdt']}/{c['gdt']} sizes {c['sizes']} chunk {c['chunk']} scaler {bool(c['scaler'])} "
-        f"clip {c['max_norm']} bad {sorted(c['bad'])} at {c['bad_pos']:.3f}")
+        f"clip {c['max_norm']} bad {sorted(c['bad'])} at {c['bad_pos']:.3f}{' MGOPT_FOLD=0' if five else ''}")
     params = []
     for i, n in enumerate(c["sizes"]):
         p = torch.empty(n, dtype=DT[c["pdt"]], device=DEV)
@@ -122,3 +128,5 @@ def test_random_configuration_against_the_oracle(seed):
             want = O.to_bf16(orc.p[k].ravel()) if c["pdt"] == "bf16" else O.to_f16(orc.p[k].ravel())
             assert np.array_equal(bits, want), (seed, k)
     assert opt._engine.device_bc_flag() == 0
+    if five:
+        assert opt._engine.folded() == 0
