@@ -184,6 +184,23 @@ def test_pass2_beyond_one_dispatch():
     _check_full(pair, "two dispatches", 2)
 
 
+def test_fp32_tensors_beyond_2gib():
+    """fp32 parameters and fp32 gradients (the class torch's own fused step
+    runs in the reference's loop on a GPU) with one tensor of 640M elements:
+    2.56 GB each for the parameter, its gradient and both moments, so every
+    stream's byte offsets pass 2^31 inside one tensor.  Heavy-tailed gradients
+    (clipping every step), GradScaler, 3 steps; both tensors bit-exact against
+    the oracle at every step."""
+    shapes = [("big", (640, 1_000_000)), ("b", (1000,))]
+    log("case: fp32 params/grads, one 640M-element tensor, 3 steps")
+    pair = Pair(Case(shapes=shapes, param_dtype="f32", grad_dtype="f32", steps=3, sigma=1e-3, tail=(1000, 100.0),
+                     scaler=dict(init_scale=1024.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=2000),
+                     subset=[0, 1], host_grads=True))
+    _run_full(pair, "fp32 beyond 2 GiB", check_at={1, 2, 3})
+    assert all(o["norm"] > 1.0 and not o["skipped"] for o in pair.outs)
+    _check_full(pair, "fp32 beyond 2 GiB", 3)
+
+
 def test_ragged_full_size():
     """20,000 tensors, log-uniform sizes 1..4M elements, 2.5B elements, fp32
     params, fp16 grads, GradScaler growth interval 50; 6 steps with a NaN at
