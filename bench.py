@@ -161,28 +161,37 @@ def read_traffic(name: str) -> float | None:
 
 
 def time_device_copy(dev: torch.device, gib: float, stream, launches: int = 6) -> dict:
-    """The runtime's device-to-device copy (torch's copy_ -> hipMemcpyAsync,
-    run as the runtime's own copy kernel) of one `gib`-GiB buffer into
-    another, timed with HIP events on `stream`; the first launch is untimed.
-    Bytes moved per launch: the buffer read once and written once."""
+    """Two reference streams over `gib`-GiB fp32 buffers, timed with HIP
+    events on `stream` (the first launch of each untimed):
+      - the runtime's device-to-device copy (torch's copy_ -> hipMemcpyAsync,
+        run as the runtime's own copy kernel): the buffer read once and
+        written once, half reads and half writes like pass 2;
+      - torch's fill kernel (fill_) over the destination: writes only.
+    Returns the copy's figures, with the fill's under "fill"."""
     n = int(gib * (1 << 30)) // 4
     src = torch.empty(n, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     src.fill_(1.0)
-    dst.copy_(src)
-    spans = []
-    for _ in range(launches):
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        dst.copy_(src)
-        b.record(stream)
-        spans.append((a, b))
-    torch.cuda.synchronize()
-    ms = sorted(a.elapsed_time(b) for a, b in spans)
+
+    def timed(op) -> list[float]:
+        op()
+        spans = []
+        for _ in range(launches):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            op()
+            b.record(stream)
+            spans.append((a, b))
+        torch.cuda.synchronize()
+        return sorted(a.elapsed_time(b) for a, b in spans)
+
+    ms = timed(lambda: dst.copy_(src))
+    fill_ms = timed(lambda: dst.fill_(2.0))
     moved = 2 * 4 * n
-    med = ms[len(ms) // 2]
-    out = {"bytes_per_launch": moved, "launches": launches, "ms": med, "ms_all": ms, "GBps": moved / (med * 1e-3) / 1e9}
+    med, fmed = ms[len(ms) // 2], fill_ms[len(fill_ms) // 2]
+    out = {"bytes_per_launch": moved, "launches": launches, "ms": med, "ms_all": ms, "GBps": moved / (med * 1e-3) / 1e9,
+           "fill": {"bytes_per_launch": 4 * n, "ms": fmed, "ms_all": fill_ms, "GBps": 4 * n / (fmed * 1e-3) / 1e9}}
     del src, dst
     torch.cuda.empty_cache()
     return out
@@ -282,8 +291,8 @@ def main() -> int:
                          "time its replays (for small sets, whose eager step is bound by the host's launches)")
     ap.add_argument("--copy-ceiling", type=float, default=0.0, metavar="GIB",
                     help="after the timed steps, also time the runtime's own device-to-device copy "
-                         "(hipMemcpyAsync, torch's copy_) of a GIB-gibibyte buffer in this process, "
-                         "and report pass 2's rate against it")
+                         "(hipMemcpyAsync, torch's copy_) of a GIB-gibibyte buffer and torch's fill of it "
+                         "(writes only) in this process, and report pass 2's rate against the copy")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB fp32 device copy (reads 1 GiB, writes 1 GiB) three times, "
                          "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -400,6 +409,8 @@ def main() -> int:
         copy = time_device_copy(dev, args.copy_ceiling, stream)
         log(f"runtime copy of {args.copy_ceiling:g} GiB: {copy['ms']:.3f} ms = {copy['GBps']:.0f} GB/s "
             f"(read + write); pass 2 runs at {adamw_gbps / copy['GBps']:.3f} of it")
+        log(f"fill of {args.copy_ceiling:g} GiB (writes only): {copy['fill']['ms']:.3f} ms = "
+            f"{copy['fill']['GBps']:.0f} GB/s")
 
     cpu = None
     if not args.no_cpu_baseline:
