@@ -480,8 +480,9 @@ class _Engine:
         the kernels.  The groups' values are compared as stored and converted
         only when one changed (a tensor lr is always re-read)."""
         groups = self.opt.param_groups
-        raw = [(g["lr"], g["weight_decay"], g["betas"], g["eps"], g.get("maximize", False), g.get("amsgrad", False))
-               for g in groups]
+        # betas copied into a tuple: a list mutated in place must not compare equal to its earlier self
+        raw = [(g["lr"], g["weight_decay"], tuple(g["betas"]), g["eps"], g.get("maximize", False),
+                g.get("amsgrad", False)) for g in groups]
         if not any(isinstance(r[0], torch.Tensor) for r in raw) and raw == self.hp_raw:
             return
         key = []

@@ -204,6 +204,28 @@ def test_hyperparameter_branches():
         assert exact_fraction(st["exp_avg_sq"].cpu().numpy(), orc.v[i]) == 1.0, i
 
 
+def test_group_values_changed_in_place_take_effect():
+    """torch reads every group's betas, eps, weight decay and lr at each step
+    (adam.py:214-272).  Betas held as a list and changed in place, and eps and
+    weight decay rewritten, between steps: the next steps use the new values,
+    bit-exact against the oracle given the same changes."""
+    shapes = [("w", (64, 33)), ("b", (33,)), ("c", (2, 700))]
+    pair = Pair(Case(shapes=shapes, steps=8, sigma=1e-2, max_norm=1.0))
+    for g in pair.opt.param_groups:
+        g["betas"] = list(g["betas"])
+    pair.run(3)
+    for g, h in zip(pair.opt.param_groups, pair.orc.hparams):
+        g["betas"][0] = 0.5
+        g["betas"][1] = 0.99
+        h["betas"] = (0.5, 0.99)
+    pair.run(5, start=4)
+    g0, h0 = pair.opt.param_groups[0], pair.orc.hparams[0]
+    g0["eps"] = h0["eps"] = 1e-4
+    g0["weight_decay"] = h0["weight_decay"] = 0.3
+    pair.run(8, start=6)
+    check_pair(pair, label="group_values_in_place")
+
+
 def _train(opt, scaler, params, steps, start=1):
     for s in range(start, start + steps):
         mg.set_optimizer_lr(opt, mg.cosine_lr(s - 1, 3e-4, 3e-5, 3, 20))
