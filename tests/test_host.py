@@ -256,6 +256,18 @@ def test_bench_refuses_more_than_one_gpu():
     assert "one GPU" in r.stderr and r.stdout == ""
 
 
+def test_bench_ab_mode_refuses_graph_capture():
+    """bench.py --ab compares eager steps of kernel builds; asked together with
+    --graph it exits with a usage error before touching any GPU."""
+    import subprocess
+    import sys as _sys
+
+    r = subprocess.run([_sys.executable, str(ROOT / "bench.py"), "--ab", "other.so", "--graph"], capture_output=True,
+                       text=True, timeout=300, cwd=str(ROOT))
+    assert r.returncode == 2
+    assert "--ab" in r.stderr and r.stdout == ""
+
+
 def test_pickled_optimizer_keeps_its_settings(mg):
     """torch pickles only defaults, state and param_groups; the settings of
     this AdamW travel too, the unpickled parameters are registered for the
