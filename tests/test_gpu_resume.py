@@ -12,8 +12,10 @@ clip_grad_norm_, step, update) on a model with MiniGPT's parameter structure
 checkpoint so the loss scale backs off in both halves.  The checkpoint is the
 dict of src/minigpt/checkpoint.py:28-52 (build_checkpoint_payload), written
 with torch.save and read back with torch.load(weights_only=True); the
-optimizer state goes back in through load_state_dict with the runtime
-options kept, as src/minigpt/optim.py:161-177 does for a native checkpoint.
+optimizer and scaler states go back in through this package's
+load_optimizer_state and load_grad_scaler_state, the calls of
+train.py:376-377 (a native checkpoint: load_state_dict with this run's
+execution options kept, src/minigpt/optim.py:161-177).
 """
 
 from __future__ import annotations
@@ -71,16 +73,6 @@ def _payload(model, opt, scaler, step):
     return out
 
 
-def _load_optimizer_state(opt, payload):
-    """The native-checkpoint branch of src/minigpt/optim.py:147-177: load, then
-    restore this run's execution options."""
-    runtime = [{k: g[k] for k in ("fused", "foreach", "capturable", "differentiable") if k in g}
-               for g in opt.param_groups]
-    opt.load_state_dict(payload)
-    for g, o in zip(opt.param_groups, runtime):
-        g.update(o)
-
-
 def _assert_equal(a, b, path):
     """Nested bitwise equality (tests/test_resume_consistency.py's assert_nested_equal)."""
     if isinstance(a, torch.Tensor):
@@ -121,8 +113,9 @@ def test_resume_from_checkpoint_is_bit_exact(dtype, tmp_path):
     ckpt = torch.load(path, map_location=DEV, weights_only=True)
     model, opt, scaler = _build(dtype, seed=123)          # different initial weights: everything comes from the file
     model.load_state_dict(ckpt["model_state"])
-    _load_optimizer_state(opt, ckpt["optimizer_state"])
-    scaler.load_state_dict(ckpt["scaler_state"])
+    # the resume calls of train.py:376-377
+    mg.load_optimizer_state(opt, ckpt["optimizer_state"], model)
+    mg.load_grad_scaler_state(scaler, ckpt["scaler_state"])
     assert mg.optimizer_completed_steps(opt) == SAVE_AT - 1
     _iterate(model, opt, scaler, data, SAVE_AT + 1, STEPS)
     resumed = _payload(model, opt, scaler, STEPS)
