@@ -72,10 +72,15 @@ def _compare(pe, oe, se, pg, og, sg, norm_e, norm_g, label):
             assert _same(oe.state[a][k], og.state[b][k]), (label, k)
 
 
+@pytest.mark.parametrize("fold", [True, False], ids=["three_kernels", "five_kernels"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_captured_step_replays_match_eager(dtype):
+def test_captured_step_replays_match_eager(dtype, fold, monkeypatch):
     """fp32 parameters, and bf16 parameters with fp32 masters (the bf16 copy
-    rewritten from the master by every replay)."""
+    rewritten from the master by every replay); the step of a small plan in
+    its three-kernel form, and in the five-kernel form of larger plans
+    (MGOPT_FOLD=0 when the plans are made)."""
+    if not fold:
+        monkeypatch.setenv("MGOPT_FOLD", "0")
     pe, oe, se = _setup(False, dtype)
     pg, og, sg = _setup(True, dtype)
     n_steps = 24
@@ -91,6 +96,7 @@ def test_captured_step_replays_match_eager(dtype):
         norm_g = _eager_step(pg, og, sg)
         _compare(pe, oe, se, pg, og, sg, norm_e, norm_g, f"eager step {s}")
 
+    assert og._engine.folded() == oe._engine.folded() == fold
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         norm_g = _eager_step(pg, og, sg)          # recorded, not run
@@ -119,7 +125,8 @@ def test_captured_step_replays_match_eager(dtype):
     assert og._engine.device_bc_flag() == 0 and og._engine.captured
     with pytest.raises(RuntimeError, match="captured"):
         og.add_param_group({"params": [torch.nn.Parameter(torch.zeros(3, device=DEV))]})
-    log(f"[graph {dtype}] 20 replays + 4 eager steps bit-exact against the eager twin; scale {sg.get_scale()}")
+    log(f"[graph {dtype} fold={fold}] 20 replays + 4 eager steps bit-exact against the eager twin; "
+        f"scale {sg.get_scale()}")
 
 
 # every refused capture ends with nothing recorded, which torch reports as an empty graph
