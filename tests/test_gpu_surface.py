@@ -34,6 +34,16 @@ def _grads(params, step, sigma, dtype=None):
         syn.fill_(p.grad, syn.GRAD_SEED, syn.grad_stream(step, i), sigma)
 
 
+@pytest.fixture(params=[True, False], ids=["three_kernels", "five_kernels"])
+def step_form(request, monkeypatch):
+    """Small plans run the step as three kernels; MGOPT_FOLD=0 when a plan is
+    made keeps the five-kernel form of larger plans.  Yields True for the
+    three-kernel form."""
+    if not request.param:
+        monkeypatch.setenv("MGOPT_FOLD", "0")
+    return request.param
+
+
 def test_first_clip_takes_the_fused_path_and_leaves_grads():
     params = _params([(300, 7), (33,)], torch.bfloat16)
     opt = mg.AdamW([{"params": params[:1], "weight_decay": 0.1}, {"params": params[1:], "weight_decay": 0.0}], lr=1e-3)
@@ -149,9 +159,10 @@ def test_grads_that_are_none_skip_their_tensor():
         assert float(ng) == out["norm"]
 
 
-def test_misaligned_views_and_odd_sizes():
+def test_misaligned_views_and_odd_sizes(step_form):
     """Parameters that start 4 bytes into their storage and sizes that are not
-    multiples of 4 run through the element-wise path of both passes."""
+    multiples of 4 run through the element-wise path of both passes, in both
+    step forms."""
     base = torch.empty(5 * 4096 + 3, device=DEV)
     syn.fill_(base, syn.PARAM_SEED, 99, 0.02)
     views = [torch.nn.Parameter(base[1:4097]), torch.nn.Parameter(base[4099:4099 + 9999])]
@@ -170,6 +181,7 @@ def test_misaligned_views_and_odd_sizes():
         opt.step()
         assert float(norm) == out["norm"]
     torch.cuda.synchronize()
+    assert opt._engine.folded() == step_form
     for i, v in enumerate(views):
         st = opt.state[v]
         assert exact_fraction(v.detach().cpu().numpy(), orc.p[i]) == 1.0
@@ -452,9 +464,10 @@ def test_launches_follow_torch_current_stream():
         assert torch.equal(a, b)
 
 
-def test_stock_torch_grad_scaler_drives_this_adamw():
+def test_stock_torch_grad_scaler_drives_this_adamw(step_form):
     """torch.amp.GradScaler hands found_inf / grad_scale to an optimizer with
-    _step_supports_amp_scaling; the results equal this package's scaler."""
+    _step_supports_amp_scaling; the results equal this package's scaler, in
+    both step forms."""
     shapes = [(300, 3), (77,)]
     out = []
     for use_stock in (False, True):
@@ -470,6 +483,7 @@ def test_stock_torch_grad_scaler_drives_this_adamw():
             sc.step(opt)   # no explicit unscale_: the scaler unscales inside step
             sc.update()
         torch.cuda.synchronize()
+        assert opt._engine.folded() == step_form
         out.append(([p.detach().clone() for p in params], sc.get_scale()))
     (pa, sa), (pb, sb) = out
     assert sa == sb
@@ -505,9 +519,9 @@ def test_scaler_stage_errors_match_torch():
     assert set(st) == {"scale", "growth_factor", "backoff_factor", "growth_interval", "_growth_tracker"}
 
 
-def test_window_metrics_replace_per_step_bookkeeping():
+def test_window_metrics_replace_per_step_bookkeeping(step_form):
     """The device window record equals what train.py:487-489,501-507 computes
-    with torch.maximum and optimizer-step differences."""
+    with torch.maximum and optimizer-step differences, in both step forms."""
     params = _params([(300, 7), (33,)])
     opt = mg.AdamW(params, lr=1e-3)
     sc = mg.GradScaler("cuda", init_scale=256.0)
@@ -521,6 +535,7 @@ def test_window_metrics_replace_per_step_bookkeeping():
         norms.append(mg.clip_grad_norm_(params, 1.0))
         sc.step(opt)
         sc.update()
+    assert opt._engine.folded() == step_form
     w = opt.window_metrics()
     ref_max = torch.zeros((), device=DEV)
     for n in norms:
@@ -566,10 +581,11 @@ def test_grad_arena_matches_fresh_gradients():
         assert torch.equal(x, y)
 
 
-def test_fp16_params_and_mixed_dtype_classes():
+def test_fp16_params_and_mixed_dtype_classes(step_form):
     """One optimizer holding fp32 params with fp32 / fp16 / bf16 grads and
     fp16 and bf16 params with fp32 masters: every (grad dtype, param kind)
-    class is its own kernel instance; all must match the oracle bit for bit."""
+    class is its own kernel instance; all must match the oracle bit for bit,
+    in both step forms."""
     specs = [  # (shape, param dtype, grad dtype)
         ((300, 5), torch.float32, torch.float32),
         ((1001,), torch.float32, torch.float16),
@@ -608,6 +624,7 @@ def test_fp16_params_and_mixed_dtype_classes():
         assert float(norm) == out["norm"] or (out["norm"] == float("inf") and float(norm) == float("inf"))
         assert sc.get_scale() == out["scale"]
     torch.cuda.synchronize()
+    assert opt._engine.folded() == step_form
     for i, p in enumerate(params):
         st = opt.state[p]
         master = st.get("master_param", p).detach().float().cpu().numpy().ravel()
@@ -620,9 +637,10 @@ def test_fp16_params_and_mixed_dtype_classes():
             assert np.array_equal(bits, ref), i
 
 
-def test_one_scaler_two_optimizers():
+def test_one_scaler_two_optimizers(step_form):
     """GradScaler.update sums the found_inf of every optimizer stepped this
-    iteration (grad_scaler.py:517-527): an inf in either one backs off."""
+    iteration (grad_scaler.py:517-527): an inf in either one backs off, in
+    both step forms."""
     pa, pb = _params([(100, 3)]), _params([(57,)])
     oa, ob = mg.AdamW(pa, lr=1e-3), mg.AdamW(pb, lr=1e-3)
     sc = mg.GradScaler("cuda", init_scale=64.0, growth_interval=2)
@@ -638,6 +656,7 @@ def test_one_scaler_two_optimizers():
             sc.step(o)
         sc.update()
         traj.append(sc.get_scale())
+    assert oa._engine.folded() == ob._engine.folded() == step_form
     assert traj == [64.0, 128.0, 64.0, 64.0, 128.0, 128.0]
     assert mg.optimizer_completed_steps(oa) == 6 and mg.optimizer_completed_steps(ob) == 5
 
