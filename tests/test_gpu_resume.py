@@ -34,6 +34,16 @@ DEV = "cuda:0"
 STEPS, SAVE_AT, INF_AT = 8, 4, (3, 6)
 
 
+@pytest.fixture(autouse=True, params=[True, False], ids=["three_kernels", "five_kernels"])
+def step_form(request, monkeypatch):
+    """Every test here runs with the step of a small plan in its three-kernel
+    form and again in the five-kernel form of larger plans (MGOPT_FOLD=0 when
+    the plans are made)."""
+    if not request.param:
+        monkeypatch.setenv("MGOPT_FOLD", "0")
+    return request.param
+
+
 def _build(dtype, seed):
     torch.manual_seed(seed)
     model = MiniGPT(dtype=dtype).to(DEV)

@@ -27,6 +27,16 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
+@pytest.fixture(autouse=True, params=[True, False], ids=["three_kernels", "five_kernels"])
+def step_form(request, monkeypatch):
+    """Every test here runs with the step of a small plan in its three-kernel
+    form and again in the five-kernel form of larger plans (MGOPT_FOLD=0 when
+    the plans are made)."""
+    if not request.param:
+        monkeypatch.setenv("MGOPT_FOLD", "0")
+    return request.param
+
+
 class Block(nn.Module):
     def __init__(self, c):
         super().__init__()
