@@ -30,6 +30,16 @@ SHAPES = [("w0", (64, 130)), ("w1", (3, 4099)), ("w2", (4096, 2)), ("b0", (7,)),
 CHUNK = 4096
 
 
+@pytest.fixture(autouse=True, params=[True, False], ids=["three_kernels", "five_kernels"])
+def step_form(request, monkeypatch):
+    """Every case runs with the step of a small plan in its three-kernel form
+    and again in the five-kernel form of larger plans (MGOPT_FOLD=0 when the
+    plans are made): their pass-1 chunks and finalize differ."""
+    if not request.param:
+        monkeypatch.setenv("MGOPT_FOLD", "0")
+    return request.param
+
+
 def test_nonfinite_at_chunk_edges_and_tails():
     """fp32 params, fp16 grads, GradScaler 65536, chunks of 4096 elements: a
     non-finite value at each edge of the work decomposition skips exactly its
