@@ -35,13 +35,18 @@ def test_synthetic_fill_matches_oracle():
                 assert np.array_equal(bits, O.to_f16(ref) if dt == "f16" else O.to_bf16(ref)), (dt, n)
 
 
-def test_tiny_cpu_workload_100_steps_bit_exact():
+@pytest.mark.parametrize("fold", [True, False], ids=["three_kernels", "five_kernels"])
+def test_tiny_cpu_workload_100_steps_bit_exact(fold, monkeypatch):
     """MiniGPT tiny_cpu shapes (52 tensors, 822,016 fp32 params), grads
     N(0,1e-3), AdamW lr 3e-4 cosine (warm-up 10), betas (0.9, 0.95), eps 1e-8,
-    wd 0.1 on matrices and embeddings, clip 1.0, 100 steps."""
-    log("case: minigpt_tiny_cpu 100 steps")
+    wd 0.1 on matrices and embeddings, clip 1.0, 100 steps; the three-kernel
+    step this small plan runs, and the five-kernel step (MGOPT_FOLD=0)."""
+    if not fold:
+        monkeypatch.setenv("MGOPT_FOLD", "0")
+    log(f"case: minigpt_tiny_cpu 100 steps, fold={fold}")
     pair = Pair(Case(shapes=mg.paramsets.WORKLOADS["minigpt_tiny_cpu"](), steps=100, sigma=1e-3))
     pair.run()
+    assert pair.opt._engine.folded() == fold
     check_pair(pair, label="tiny_cpu")
 
 
