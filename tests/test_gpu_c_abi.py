@@ -86,8 +86,14 @@ def _bc_table(betas, cap):
     return torch.tensor(out, dtype=torch.float64, device=DEV)
 
 
-def test_three_kernel_classes_through_the_raw_abi():
+@pytest.mark.parametrize("fold", [True, False], ids=["three_kernels", "five_kernels"])
+def test_three_kernel_classes_through_the_raw_abi(fold, monkeypatch):
+    """In the three-kernel form this small plan runs, and in the five-kernel
+    form (MGOPT_FOLD=0 when the plan is made; mgopt_plan_folded reports it)."""
+    if not fold:
+        monkeypatch.setenv("MGOPT_FOLD", "0")
     lib = _lib()
+    lib.mgopt_plan_folded.argtypes = [ctypes.c_void_p]
     specs = [  # (numel, param dtype, grad dtype, group)
         (5000, torch.float32, torch.float32, 0),
         (70000, torch.bfloat16, torch.bfloat16, 0),     # two chunks, bf16 model copy + fp32 master
@@ -116,6 +122,7 @@ def test_three_kernel_classes_through_the_raw_abi():
     plan = ctypes.c_void_p()
     _ok(lib.mgopt_plan_create(descs, len(specs), 2, steps.data_ptr(), 65536, ctypes.byref(plan)), lib, "create")
     try:
+        assert lib.mgopt_plan_folded(plan) == (1 if fold else 0)
         _ok(lib.mgopt_sync_master(plan, _stream()), lib, "sync_master")
         scale = torch.full((), 1024.0, dtype=torch.float32, device=DEV)
         tracker = torch.zeros((), dtype=torch.int32, device=DEV)
