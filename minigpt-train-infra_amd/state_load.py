@@ -1,211 +1,268 @@
-"""Loading checkpointed optimizer and GradScaler state.
+"""Loading checkpointed optimizer and GradScaler state on resume.
 
-The two loaders the reference's training loop calls on resume
-(train.py:376-377), with the behaviour of src/minigpt/optim.py:74-273, so
-that a loop can import them from this package with the rest of its helpers.
+The reference's training loop restores its optimizer and scaler through two
+loaders (train.py:376-377; behaviour at src/minigpt/optim.py:136-273).  This
+module gives a loop the same two calls with the same accepted inputs, built as
+three stages:
 
-load_optimizer_state accepts the three checkpoint forms the reference accepts:
-  - torch's state_dict whose groups match the optimizer's (same group sizes,
-    and the same param_names or a single group on both sides): loaded with
-    optimizer.load_state_dict, after which the execution flags of this run's
-    groups (fused, foreach, capturable, differentiable) are put back
-    (optim.py:147-177);
-  - torch's state_dict of another grouping, such as a single group over
-    model.parameters(), or one saved before the q/k/v projections were fused
-    into qkv_proj: states are matched to parameters by name, the hyper-
-    parameters are taken from the saved groups, and the q/k/v states of a
-    fused projection are concatenated (optim.py:179-216, 229-251);
-  - the teaching version's format: a list with one state per parameter in
-    model order, a global step_num and scalar hyper-parameters
-    (optim.py:217-240).
+  1. classify the payload once (`_classify`): torch's state_dict laid out as
+     this optimizer's groups ("native"), torch's state_dict of another
+     grouping ("by_name"), or the teaching version's per-parameter list
+     ("list");
+  2. resolve a non-native payload into a `_Resolved` record: every saved state
+     keyed by parameter name, plus the hyper-parameters and per-group weight
+     decays the groups take on (`_resolve_by_name`, `_resolve_list`);
+  3. install the record into the optimizer (`_install`): each parameter takes
+     the state saved under its name; a fused q/k/v projection saved as three
+     separate projections takes their states joined along dim 0; a parameter
+     with neither starts from fresh state.
 
-One difference, on purpose.  The reference moves every migrated state tensor
-to the parameter's dtype (optim.py:124-133).  This package's AdamW keeps
+Saved states without a param_names list are in model registration order,
+either of the current model or of the same model before its q/k/v
+projections were fused (`_QkvLayout`).
+
+One difference, on purpose: the reference moves every migrated state tensor to
+the parameter's dtype (optim.py:124-133).  This package's AdamW keeps
 exp_avg, exp_avg_sq and master_param in fp32 whatever the parameter dtype, so
-for bf16/fp16 parameters those three are moved to the device in fp32 rather
-than rounded to the parameter's dtype first.  For fp32 parameters, and for
-optimizers other than this package's AdamW, the two agree.
+for its bf16/fp16 parameters those three stay fp32.  For fp32 parameters, and
+for optimizers other than this package's AdamW, the two agree.
 """
 
 from __future__ import annotations
 
-from typing import Any
+import re
+from dataclasses import dataclass
+from typing import Any, Callable
 
 import torch
 
 from .adamw import AdamW
 
-#: group options that select an execution path, kept from the current run
-_EXEC_FLAGS = ("fused", "foreach", "capturable", "differentiable")
-#: group hyper-parameters a migration takes from the checkpoint
-_HPARAMS = ("lr", "betas", "eps", "amsgrad", "maximize")
-_PROJECTIONS = ("q_proj", "k_proj", "v_proj")
-#: state tensors this package's AdamW keeps in fp32
-_FP32_STATE = frozenset(("exp_avg", "exp_avg_sq", "master_param"))
+#: group options that pick an execution path on this machine: the current
+#: run's values survive a native load
+_RUNTIME_OPTIONS = ("fused", "foreach", "capturable", "differentiable")
+#: hyper-parameters every group takes from a migrated checkpoint
+_SHARED_HPARAMS = ("lr", "betas", "eps", "amsgrad", "maximize")
+#: state entries this package's AdamW holds in fp32 for any parameter dtype
+_FP32_ENTRIES = frozenset(("exp_avg", "exp_avg_sq", "master_param"))
+
+#: a fused attention projection: stem, then weight or bias
+_FUSED_QKV = re.compile(r"^(?P<stem>.*\.attn\.)qkv_proj\.(?P<kind>weight|bias)$")
+_SEPARATE_PROJECTIONS = ("q_proj", "k_proj", "v_proj")
+
+#: the teaching version's scaler keys -> torch's state_dict keys and types
+_TEACHING_SCALER = {
+    "scale": ("scale", float),
+    "growth_factor": ("growth_factor", float),
+    "backoff_factor": ("backoff_factor", float),
+    "growth_interval": ("growth_interval", int),
+    "_growth_tracker": ("growth_tracker", int),
+}
 
 
-def _optimizer_parameter_names(optimizer: torch.optim.Optimizer, model: torch.nn.Module) -> list[tuple[str, Any]]:
-    """(name, parameter) for every parameter of the optimizer, in its group
-    order, named as model.named_parameters() names it."""
-    name_of = {id(p): n for n, p in model.named_parameters()}
+class _QkvLayout:
+    """A model's trainable parameter names in registration order, as they are
+    and as they were before each attention's q/k/v projections were fused
+    into one qkv_proj (weight and bias of q_proj, k_proj and v_proj, in that
+    order, in place of qkv_proj.weight; nothing in place of qkv_proj.bias)."""
+
+    def __init__(self, model: torch.nn.Module):
+        self.current = [n for n, p in model.named_parameters() if p.requires_grad]
+        self.separate: list[str] = []
+        #: fused name -> the three separate names its state is joined from
+        self.parts: dict[str, list[str]] = {}
+        for name in self.current:
+            hit = _FUSED_QKV.match(name)
+            if hit is None:
+                self.separate.append(name)
+                continue
+            stem, kind = hit["stem"], hit["kind"]
+            self.parts[name] = [f"{stem}{proj}.{kind}" for proj in _SEPARATE_PROJECTIONS]
+            if kind == "weight":
+                self.separate += [f"{stem}{proj}.{k}" for proj in _SEPARATE_PROJECTIONS for k in ("weight", "bias")]
+
+    def names_for(self, count: int) -> list[str]:
+        """The layout that `count` saved states were written in."""
+        for layout in (self.current, self.separate):
+            if len(layout) == count:
+                return layout
+        raise ValueError(f"load_optimizer_state: {count} saved states fit neither the model's "
+                         f"{len(self.current)} trainable parameters nor the {len(self.separate)} of its layout "
+                         f"before the q/k/v fusion")
+
+
+@dataclass
+class _Resolved:
+    """A migrated checkpoint: saved states by parameter name, the
+    hyper-parameters every group takes on, and the weight decay of a group
+    given its group_name."""
+
+    by_name: dict[str, dict[str, Any]]
+    hparams: dict[str, Any]
+    decay_of: Callable[[Any, float], float]
+
+
+def _named_optimizer_params(optimizer: torch.optim.Optimizer, model: torch.nn.Module) -> list[tuple[str, Any]]:
+    """(model name, parameter) for each parameter of the optimizer, in its
+    param_groups order."""
+    names = {id(p): n for n, p in model.named_parameters()}
     out = []
-    for group in optimizer.param_groups:
-        for p in group["params"]:
-            if id(p) not in name_of:
-                raise ValueError("Optimizer contains a parameter that is not present in the model")
-            out.append((name_of[id(p)], p))
+    for p in (p for group in optimizer.param_groups for p in group["params"]):
+        if id(p) not in names:
+            raise ValueError("load_optimizer_state: the optimizer holds a parameter that model.named_parameters() "
+                             "does not yield")
+        out.append((names[id(p)], p))
     return out
 
 
-def _unfused_names(names: list[str]) -> list[str]:
-    """The parameter names of the same model before the q/k/v projections were
-    fused: each attn.qkv_proj.weight stands for q_proj, k_proj and v_proj,
-    weight and bias each, in that order; attn.qkv_proj.bias stands for
-    nothing more."""
-    out: list[str] = []
-    for name in names:
-        if name.endswith(".attn.qkv_proj.bias"):
-            continue
-        if name.endswith(".attn.qkv_proj.weight"):
-            stem = name[: -len("qkv_proj.weight")]
-            out.extend(f"{stem}{proj}.{kind}" for proj in _PROJECTIONS for kind in ("weight", "bias"))
-        else:
-            out.append(name)
-    return out
+def _group_sizes(groups: list[dict[str, Any]]) -> list[int]:
+    return [len(g["params"]) for g in groups]
 
 
-def _names_for_model_order(model: torch.nn.Module, count: int) -> list[str]:
-    """Names of `count` states saved in model order: the model's trainable
-    parameters as they are, or as they were before the QKV fusion."""
-    current = [n for n, p in model.named_parameters() if p.requires_grad]
-    if count == len(current):
-        return current
-    unfused = _unfused_names(current)
-    if count == len(unfused):
-        return unfused
-    raise ValueError("Optimizer state does not match current or separate-QKV model parameters")
+def _group_names(groups: list[dict[str, Any]]) -> list[str]:
+    return [n for g in groups for n in g.get("param_names", ())]
 
 
-def _fused_projection_state(name: str, states: dict[str, dict[str, Any]]) -> dict[str, Any]:
-    """State of a fused qkv_proj weight or bias from the saved q/k/v states:
-    tensors with dimensions are concatenated along dim 0, anything else (the
-    step) is taken from q_proj.  Empty when any of the three is empty."""
-    kind = "weight" if name.endswith("qkv_proj.weight") else "bias"
-    stem = name[: -len(f"qkv_proj.{kind}")]
-    parts = [states[f"{stem}{proj}.{kind}"] for proj in _PROJECTIONS]
+def _classify(payload: dict[str, Any], optimizer: torch.optim.Optimizer, n_params: int) -> str:
+    """'native' (load as it is), 'by_name' (torch format, other grouping) or
+    'list' (teaching format)."""
+    if "param_groups" not in payload:
+        if isinstance(payload.get("state"), list):
+            return "list"
+        raise ValueError("load_optimizer_state: unrecognised checkpoint; expected torch's optimizer state_dict or "
+                         "a list of per-parameter states with step_num and scalar hyper-parameters")
+    saved, mine = payload["param_groups"], optimizer.param_groups
+    sizes = _group_sizes(saved)
+    if sum(sizes) != n_params or sizes != _group_sizes(mine):
+        return "by_name"
+    saved_names = _group_names(saved)
+    if saved_names and saved_names == _group_names(mine):
+        return "native"
+    return "native" if len(saved) == 1 and len(mine) == 1 else "by_name"
+
+
+def _load_native(optimizer: torch.optim.Optimizer, payload: dict[str, Any]) -> None:
+    """load_state_dict, then this run's execution options back on every group
+    (a checkpoint written on a CPU must not switch off the fused path here)."""
+    runtime = [{k: g[k] for k in _RUNTIME_OPTIONS if k in g} for g in optimizer.param_groups]
+    optimizer.load_state_dict(payload)
+    for group, options in zip(optimizer.param_groups, runtime):
+        group.update(options)
+
+
+def _resolve_by_name(payload: dict[str, Any], layout: _QkvLayout) -> _Resolved:
+    """torch's state_dict of another grouping: saved states named by the saved
+    param_names, else by model order (the checkpoint predates the grouping);
+    the first saved group's hyper-parameters; weight decay per group_name."""
+    saved = payload["param_groups"]
+    ids = [pid for g in saved for pid in g["params"]]
+    names = _group_names(saved)
+    if names and len(names) != len(ids):
+        raise ValueError(f"load_optimizer_state: the checkpoint lists {len(names)} param_names for "
+                         f"{len(ids)} saved parameter ids")
+    if not names:
+        names = layout.names_for(len(ids))
+    stored = payload["state"]
+    by_name = {name: stored.get(pid, {}) for name, pid in zip(names, ids)}
+    named_decay = {g["group_name"]: g["weight_decay"] for g in saved if isinstance(g.get("group_name"), str)}
+    first = saved[0]
+
+    def decay_of(group_name, current):
+        if group_name in named_decay:
+            return named_decay[group_name]
+        if group_name == "no_decay":
+            return 0.0
+        return first.get("weight_decay", current)
+
+    return _Resolved(by_name, {k: first[k] for k in _SHARED_HPARAMS if k in first}, decay_of)
+
+
+def _resolve_list(payload: dict[str, Any], layout: _QkvLayout) -> _Resolved:
+    """The teaching format: one state per parameter in model order, one global
+    step_num, scalar lr / beta1 / beta2 / eps / weight_decay."""
+    entries = payload["state"]
+    names = layout.names_for(len(entries))
+    step = torch.tensor(float(payload["step_num"]), dtype=torch.float32)
+    hparams = {"lr": float(payload["lr"]), "betas": (float(payload["beta1"]), float(payload["beta2"])),
+               "eps": float(payload["eps"])}
+    decay = float(payload["weight_decay"])
+
+    def decay_of(group_name, current):
+        return 0.0 if group_name == "no_decay" else decay
+
+    return _Resolved({name: dict(entry, step=step) for name, entry in zip(names, entries)}, hparams, decay_of)
+
+
+def _joined(parts: list[dict[str, Any]]) -> dict[str, Any]:
+    """One fused projection's state from its three separate states: tensors
+    with dimensions joined along dim 0, anything else (the step count) from
+    the first.  Empty when a part has no state."""
     if not all(parts):
         return {}
-    fused: dict[str, Any] = {}
-    for key, first in parts[0].items():
+    head = parts[0]
+    out = {}
+    for key in head:
         values = [part[key] for part in parts]
-        fused[key] = torch.cat(values, dim=0) if isinstance(first, torch.Tensor) and first.ndim > 0 else first
-    return fused
-
-
-def _on_parameter_device(state: dict[str, Any], param: torch.Tensor, keep_fp32: bool) -> dict[str, Any]:
-    """The state moved to the parameter's device: the step count in fp32,
-    other tensors in the parameter's dtype, except the fp32 state of this
-    package's AdamW when keep_fp32."""
-    out: dict[str, Any] = {}
-    for key, value in state.items():
-        if not isinstance(value, torch.Tensor):
-            out[key] = value
-        elif key == "step" or (keep_fp32 and key in _FP32_STATE):
-            out[key] = value.to(device=param.device, dtype=torch.float32)
-        else:
-            out[key] = value.to(device=param.device, dtype=param.dtype)
+        joinable = isinstance(head[key], torch.Tensor) and head[key].dim() > 0
+        out[key] = torch.cat(values) if joinable else head[key]
     return out
 
 
-def load_optimizer_state(optimizer: torch.optim.Optimizer, payload: dict[str, Any], model: torch.nn.Module) -> None:
-    """Loads a checkpointed optimizer state into `optimizer`, whose parameters
-    belong to `model` (src/minigpt/optim.py:136-251; the three accepted forms
-    are listed in the module docstring).  Raises ValueError for a parameter
-    the model does not own, for param_names that do not match the saved
-    parameter ids, for a state list that fits neither the current nor the
-    pre-fusion parameter list, and for an unknown format."""
-    named = _optimizer_parameter_names(optimizer, model)
-    if "param_groups" in payload:
-        saved_groups = payload["param_groups"]
-        current_groups = optimizer.state_dict()["param_groups"]
-        saved_ids = [pid for group in saved_groups for pid in group["params"]]
-        saved_names = [n for group in saved_groups for n in group.get("param_names", [])]
-        current_names = [n for group in current_groups for n in group.get("param_names", [])]
-        same_sizes = len(saved_groups) == len(current_groups) and all(
-            len(s["params"]) == len(c["params"]) for s, c in zip(saved_groups, current_groups))
-        same_layout = (bool(saved_names) and saved_names == current_names) or (
-            len(saved_groups) == 1 and len(current_groups) == 1)
-        if len(saved_ids) == len(named) and same_sizes and same_layout:
-            flags = [{k: group[k] for k in _EXEC_FLAGS if k in group} for group in optimizer.param_groups]
-            optimizer.load_state_dict(payload)
-            for group, kept in zip(optimizer.param_groups, flags):
-                group.update(kept)
-            return
-        if saved_names:
-            if len(saved_names) != len(saved_ids):
-                raise ValueError("Optimizer checkpoint param_names do not match saved parameter IDs")
-            source_names = saved_names
-        else:
-            # saved before the decay / no_decay split: model registration order
-            source_names = _names_for_model_order(model, len(saved_ids))
-        states = {name: payload["state"].get(pid, {}) for name, pid in zip(source_names, saved_ids)}
-        hparams = saved_groups[0]
-        saved_by_group = {g["group_name"]: g for g in saved_groups if isinstance(g.get("group_name"), str)}
-    else:
-        entries = payload.get("state")
-        if not isinstance(entries, list):
-            raise ValueError("Unsupported optimizer checkpoint format")
-        source_names = _names_for_model_order(model, len(entries))
-        step = torch.tensor(float(payload["step_num"]), dtype=torch.float32)
-        states = {name: {"step": step, **entry} for name, entry in zip(source_names, entries)}
-        hparams = {
-            "lr": float(payload["lr"]),
-            "betas": (float(payload["beta1"]), float(payload["beta2"])),
-            "eps": float(payload["eps"]),
-            "weight_decay": float(payload["weight_decay"]),
-        }
-        saved_by_group = {}
+def _placed(entry: dict[str, Any], param: torch.Tensor, keep_fp32: bool) -> dict[str, Any]:
+    """Entry tensors copied to the parameter's device: the step count and (for
+    this package's AdamW) its fp32 entries in fp32, others in the parameter's
+    dtype."""
+    def place(key: str, value: Any) -> Any:
+        if not isinstance(value, torch.Tensor):
+            return value
+        fp32 = key == "step" or (keep_fp32 and key in _FP32_ENTRIES)
+        return value.to(device=param.device, dtype=torch.float32 if fp32 else param.dtype)
 
+    return {key: place(key, value) for key, value in entry.items()}
+
+
+def _install(optimizer: torch.optim.Optimizer, record: _Resolved, named: list[tuple[str, Any]],
+             layout: _QkvLayout) -> None:
     for group in optimizer.param_groups:
-        group.update({k: hparams[k] for k in _HPARAMS if k in hparams})
-        name = group.get("group_name")
-        if name in saved_by_group:
-            group["weight_decay"] = saved_by_group[name]["weight_decay"]
-        elif name == "no_decay":
-            group["weight_decay"] = 0.0
-        elif "weight_decay" in hparams:
-            group["weight_decay"] = hparams["weight_decay"]
-
+        group.update(record.hparams)
+        group["weight_decay"] = record.decay_of(group.get("group_name"), group["weight_decay"])
     keep_fp32 = isinstance(optimizer, AdamW)
     optimizer.state.clear()
     for name, param in named:
-        if name in states:
-            state = states[name]
-        elif name.endswith(("qkv_proj.weight", "qkv_proj.bias")):
-            state = _fused_projection_state(name, states)
-        else:
-            state = {}
-        if state:
-            optimizer.state[param] = _on_parameter_device(state, param, keep_fp32)
+        entry = record.by_name.get(name)
+        if entry is None and name in layout.parts:
+            entry = _joined([record.by_name.get(part, {}) for part in layout.parts[name]])
+        if entry:
+            optimizer.state[param] = _placed(entry, param, keep_fp32)
+
+
+def load_optimizer_state(optimizer: torch.optim.Optimizer, payload: dict[str, Any], model: torch.nn.Module) -> None:
+    """Restores a checkpointed optimizer state into `optimizer`, whose
+    parameters belong to `model` (the call of train.py:376; accepted forms in
+    the module docstring).  Raises ValueError for an optimizer parameter the
+    model does not own, for a checkpoint whose param_names and saved ids
+    disagree in number, for saved states that fit neither of the model's
+    layouts, and for an unrecognised payload."""
+    named = _named_optimizer_params(optimizer, model)
+    form = _classify(payload, optimizer, len(named))
+    if form == "native":
+        _load_native(optimizer, payload)
+        return
+    layout = _QkvLayout(model)
+    record = _resolve_list(payload, layout) if form == "list" else _resolve_by_name(payload, layout)
+    _install(optimizer, record, named, layout)
 
 
 def load_grad_scaler_state(scaler, payload: dict[str, Any]) -> None:
-    """Loads a checkpointed GradScaler state (src/minigpt/optim.py:254-273):
-    torch's five-key state dict as it is, or the teaching version's form
-    (enabled, scale, growth factors, growth_interval, growth_tracker).
-    Nothing happens for a disabled scaler, an empty payload, or a payload
-    saved from a disabled scaler."""
+    """Restores a checkpointed GradScaler state (the call of train.py:377):
+    torch's state_dict, or the teaching version's form (enabled, scale,
+    growth_factor, backoff_factor, growth_interval, growth_tracker), which is
+    translated to torch's keys first.  A disabled scaler, an empty payload and
+    a teaching payload saved with the scaler off leave the scaler as it is."""
     if not scaler.is_enabled() or not payload:
         return
-    if "_growth_tracker" in payload:
-        scaler.load_state_dict(payload)
-        return
-    if not payload.get("enabled", False):
-        return
-    scaler.load_state_dict({
-        "scale": float(payload["scale"]),
-        "growth_factor": float(payload["growth_factor"]),
-        "backoff_factor": float(payload["backoff_factor"]),
-        "growth_interval": int(payload["growth_interval"]),
-        "_growth_tracker": int(payload["growth_tracker"]),
-    })
+    if "_growth_tracker" not in payload:
+        if not payload.get("enabled", False):
+            return
+        payload = {key: cast(payload[old]) for key, (old, cast) in _TEACHING_SCALER.items()}
+    scaler.load_state_dict(payload)
