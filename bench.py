@@ -12,7 +12,6 @@ exp_avg_sq (131 GB resident), synthetic data.  Prints one JSON line.
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
     python bench.py --workload uniform_262144x16 --no-cpu-baseline   # 16 fp32 tensors of 16,384 elements
     python bench.py --vs-torch [--workload NAME]   # torch's own GPU step beside this one
-    python bench.py --ab other/libmgopt.so [--workload NAME] --steps 20   # kernel builds compared in one process
 """
 
 from __future__ import annotations
@@ -266,53 +265,6 @@ def vs_torch(name: str, steps: int, warmup: int, dev: torch.device) -> dict:
     }
 
 
-def ab_libraries(args, eng, one_step, ev) -> dict:
-    """--ab: the engine's two per-step entry points (mgopt_grad_norm, pass 1 +
-    finalize; mgopt_adamw_step, prologue + pass 2) are taken from each library
-    in turn, on the plan and buffers the package built, so that kernel
-    variants are compared without the spread between processes and
-    allocations.  The rounds alternate their order.  Every library must be
-    built from the same C ABI and plan layout as the package's."""
-    import ctypes
-
-    N = importlib.import_module("minigpt-train-infra_amd._native")
-    libs = {"package": (eng._grad_norm, eng._adamw_step)}
-    for path in args.ab:
-        lib = ctypes.CDLL(str(Path(path).resolve()))
-        N._declare(lib)
-        libs[path] = (lib.mgopt_grad_norm, lib.mgopt_adamw_step)
-    times: dict[str, list[tuple[float, float]]] = {k: [] for k in libs}
-    for name, fns in libs.items():       # one untimed round each
-        eng._grad_norm, eng._adamw_step = fns
-        for _ in range(2):
-            one_step(False)
-    for r in range(args.ab_rounds):
-        order = list(libs) if r % 2 == 0 else list(libs)[::-1]
-        for name in order:
-            eng._grad_norm, eng._adamw_step = libs[name]
-            ev["norm"].clear()
-            ev["adamw"].clear()
-            for _ in range(args.steps):
-                one_step(True)
-            torch.cuda.synchronize()
-            norm = sorted(a.elapsed_time(b) for a, b in ev["norm"])
-            adamw = sorted(a.elapsed_time(b) for a, b in ev["adamw"])
-            times[name].append((norm[len(norm) // 2], adamw[len(adamw) // 2]))
-            log(f"round {r} {name}: norm {times[name][-1][0]:.4f} ms, AdamW {times[name][-1][1]:.4f} ms")
-    eng._grad_norm, eng._adamw_step = libs["package"]
-    if eng.device_bc_flag() != 0:
-        raise RuntimeError("a step evaluated bias corrections on the device")
-
-    def med(xs):
-        return sorted(xs)[len(xs) // 2]
-
-    return {
-        "ab": args.workload, "rounds": args.ab_rounds, "steps_per_round": args.steps,
-        "median_ms": {k: {"norm": med([t[0] for t in v]), "adamw": med([t[1] for t in v])} for k, v in times.items()},
-        "rounds_ms": {k: v for k, v in times.items()},
-    }
-
-
 def _workload_name(name: str) -> str:
     try:
         workload_spec(name)
@@ -341,18 +293,10 @@ def main() -> int:
                     help="after the timed steps, also time the runtime's own device-to-device copy "
                          "(hipMemcpyAsync, torch's copy_) of a GIB-gibibyte buffer and torch's fill of it "
                          "(writes only) in this process, and report pass 2's rate against the copy")
-    ap.add_argument("--ab", nargs="+", default=None, metavar="LIB",
-                    help="instead of the benchmark line, compare kernel builds in one process: each LIB is another "
-                         "build of libmgopt.so (same C ABI); every round runs --steps steps with the package's "
-                         "library and with each LIB in turn on the same plan and buffers, and the median norm and "
-                         "AdamW pass times per library are printed as one JSON line")
-    ap.add_argument("--ab-rounds", type=int, default=6, metavar="R", help="rounds of --ab (default 6)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB fp32 device copy (reads 1 GiB, writes 1 GiB) three times, "
                          "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
-    if args.ab and args.graph:
-        ap.error("--ab compares eager steps; it does not combine with --graph")
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the optimizer step here has no multi-GPU path (use --gpus 1)", file=sys.stderr)
         return 2
@@ -413,9 +357,6 @@ def main() -> int:
     for _ in range(args.warmup):
         one_step(False)
     torch.cuda.synchronize()
-    if args.ab:
-        print(json.dumps(ab_libraries(args, eng, one_step, ev)), flush=True)
-        return 0
     if args.graph:
         # the whole step (unscale_, clip_grad_norm_, step, update) in one HIP
         # graph; each timed step refreshes the learning rate and replays it
