@@ -375,6 +375,30 @@ ORC_API void orc_adamw(float* p, const float* g, float* m, float* v, int64_t n,
     }
 }
 
+/* One tensor's share of an iteration whose step is taken, as OracleRun.step
+ * performs it: orc_unscale (when `unscale`), then orc_scale by the clip
+ * coefficient (when `clip`), then orc_adamw.  The tensor is processed in
+ * blocks of ORC_BLOCK elements through a stack buffer, each block through
+ * exactly those three functions, so the result is bit for bit that of the
+ * three calls over the whole tensor (tests/test_oracle_pinning.py checks
+ * it); the blocking keeps the unscaled gradient in cache instead of in a
+ * tensor-sized array. */
+#define ORC_BLOCK 2048
+ORC_API void orc_unscale_clip_adamw(const float* g, float* p, float* m, float* v, int64_t n,
+                                    float inv, int unscale, float coef, int clip,
+                                    double lr, double beta1, double beta2, double eps, double wd,
+                                    double step, int maximize) {
+    float buf[ORC_BLOCK];
+    float found = 0.0f;
+    for (int64_t s = 0; s < n; s += ORC_BLOCK) {
+        const int64_t k = n - s < ORC_BLOCK ? n - s : ORC_BLOCK;
+        if (unscale) orc_unscale(g + s, buf, k, inv, &found);
+        else memcpy(buf, g + s, (size_t)k * sizeof(float));
+        if (clip) orc_scale(buf, k, coef);
+        orc_adamw(p + s, buf, m + s, v + s, k, lr, beta1, beta2, eps, wd, step, maximize);
+    }
+}
+
 /* Deliberately wrong variants of orc_adamw, used only by the pinning tests to
  * show that the golden checks reject plausible mistakes:
  *   1: drops the bias correction of the first moment
