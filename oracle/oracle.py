@@ -61,6 +61,8 @@ def lib() -> ctypes.CDLL:
             "orc_bias_corrections": (None, [dbl, dbl, dbl, _D]),
             "orc_adamw": (None, [_F, _F, _F, _F, i64, dbl, dbl, dbl, dbl, dbl, dbl, ctypes.c_int]),
             "orc_adamw_mutant": (None, [_F, _F, _F, _F, i64, dbl, dbl, dbl, dbl, dbl, dbl, ctypes.c_int]),
+            "orc_unscale_clip_adamw": (None, [_F, _F, _F, _F, i64, ctypes.c_float, ctypes.c_int, ctypes.c_float,
+                                              ctypes.c_int, dbl, dbl, dbl, dbl, dbl, dbl, ctypes.c_int]),
             "orc_scaler_update": (None, [_F, ctypes.POINTER(i32), ctypes.c_float, dbl, dbl, i32]),
             "orc_cosine_lr": (dbl, [i64, dbl, dbl, i64, i64]),
         }
@@ -212,24 +214,38 @@ _GRAD_DTYPE = {"f32": 0, "f16": 1, "bf16": 2}
 
 
 def synth_grad(n: int, seed: int, stream: int, k: float, dtype: str = "f32", tail_every: int = 0,
-               tail_mult: float = 1.0, threads: int = 16, piece: int = 1 << 22) -> np.ndarray:
+               tail_mult: float = 1.0, threads: int = 16, piece: int = 1 << 22,
+               out: np.ndarray | None = None) -> np.ndarray:
     """The synthetic gradient the GPU generator writes into a `dtype` tensor
-    (mgopt_synth_fill), as fp32 values, generated in parallel pieces."""
+    (mgopt_synth_fill), as fp32 values, generated in parallel pieces; written
+    into `out` (float32, at least n elements; its first n are returned) when
+    given, so that a caller can reuse one buffer across steps."""
     from concurrent.futures import ThreadPoolExecutor
 
     L = lib()
     L.orc_synth_grad.restype = None
     L.orc_synth_grad.argtypes = [_F, ctypes.c_int64, ctypes.c_int64, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double,
                                  ctypes.c_uint64, ctypes.c_double, ctypes.c_int]
-    out = np.empty(n, np.float32)
+    if out is None:
+        out = np.empty(n, np.float32)
+    else:
+        assert out.dtype == np.float32 and out.flags.c_contiguous and out.size >= n
+        out = out[:n]
     code = _GRAD_DTYPE[dtype]
 
     def run(s):
         e = min(n, s + piece)
         L.orc_synth_grad(out[s:].ctypes.data_as(_F), s, e, seed, stream, k, tail_every, tail_mult, code)
 
-    with ThreadPoolExecutor(max_workers=max(1, threads)) as ex:
-        list(ex.map(run, range(0, n, piece)))
+    if n <= piece:
+        if n:
+            run(0)
+        return out
+    if threads == THREADS:
+        list(pool().map(run, range(0, n, piece)))
+    else:
+        with ThreadPoolExecutor(max_workers=max(1, threads)) as ex:
+            list(ex.map(run, range(0, n, piece)))
     return out
 
 
@@ -288,6 +304,46 @@ def adamw(p, g, m, v, lr, beta1, beta2, eps, wd, step, maximize=False) -> None:
 
 PIECE = 1 << 22          # elements per piece of the parallel element-wise helpers
 THREADS = 16             # threads of the parallel helpers (the GPU box's CPU share)
+_POOL = None
+
+
+def pool():
+    """The module's persistent pool of THREADS worker threads (the C calls
+    release the GIL), shared by the parallel helpers that run often."""
+    global _POOL
+    if _POOL is None:
+        from concurrent.futures import ThreadPoolExecutor
+
+        _POOL = ThreadPoolExecutor(max_workers=THREADS)
+    return _POOL
+
+
+def unscale_clip_adamw(g, p, m, v, inv, unscale, coef, lr, beta1, beta2, eps, wd, step, maximize=False) -> None:
+    """One tensor's update in an iteration whose step is taken, in place on
+    p, m, v: unscale by inv (when unscale), scale by coef (when coef is not
+    None), then AdamW with the new step count.  Bit for bit what unscale(),
+    scale_() and adamw() give in turn (pinned by test_oracle_pinning)."""
+    lib().orc_unscale_clip_adamw(_fp(g), _fp(p), _fp(m), _fp(v), p.size, inv, int(unscale),
+                                 1.0 if coef is None else coef, int(coef is not None), lr, beta1, beta2, eps, wd,
+                                 float(step), int(maximize))
+
+
+def unscale_clip_adamw_many(jobs, piece: int = PIECE) -> None:
+    """unscale_clip_adamw over many tensors on the module's thread pool:
+    jobs holds (g, p, m, v, kwargs) per tensor; tensors above `piece` elements
+    are split into pieces (the update is element-wise, so the bits do not
+    depend on the split)."""
+    tasks = []
+    for g, p, m, v, kw in jobs:
+        fg, fp, fm, fv = (a.reshape(-1) for a in (g, p, m, v))
+        for s in range(0, fp.size, piece):
+            e = min(fp.size, s + piece)
+            tasks.append((fg[s:e], fp[s:e], fm[s:e], fv[s:e], kw))
+    if len(tasks) == 1:
+        g, p, m, v, kw = tasks[0]
+        unscale_clip_adamw(g, p, m, v, **kw)
+        return
+    list(pool().map(lambda t: unscale_clip_adamw(t[0], t[1], t[2], t[3], **t[4]), tasks))
 
 
 def _pieces(n: int, fn, threads: int = THREADS, piece: int = PIECE) -> None:
@@ -378,6 +434,18 @@ class OracleRun:
     def lowp_params(self) -> list[np.ndarray]:
         return [round_to(x, self.lowp) for x in self.p] if self.lowp else self.p
 
+    def load(self, i: int, p: np.ndarray, m: np.ndarray, v: np.ndarray, step: float) -> None:
+        """Takes over tensor i's state from elsewhere (the GPU's, before a
+        step): the arrays are used in place, not copied."""
+        for a in (p, m, v):
+            assert a.dtype == np.float32 and a.flags.c_contiguous
+        self.p[i], self.m[i], self.v[i], self.steps[i] = p, m, v, float(step)
+
+    def unload(self, i: int) -> None:
+        """Forgets tensor i's state (its arrays are released)."""
+        empty = np.zeros(0, np.float32)
+        self.p[i], self.m[i], self.v[i] = empty, empty, empty
+
     def step(self, grads: list[np.ndarray | None], lr: float | list[float], subset=None,
              norm_override: float | None = None, totals: tuple[float, bool] | None = None) -> dict:
         """grads: fp32 values as the GPU reads them (scaled, when the scaler is
@@ -390,6 +458,8 @@ class OracleRun:
         A sum of squares of None leaves the norm unverified (out["norm"] is
         None): the clip then uses norm_override, which must be given."""
         lrs = lr if isinstance(lr, list) else [lr] * len(self.hparams)
+        if totals is not None:
+            return self._step_from_totals(grads, lrs, subset, norm_override, totals)
         found = False
         work = []
         inv = inv_scale(self.scale) if self.scaler else 1.0
@@ -403,17 +473,9 @@ class OracleRun:
             else:
                 work.append(np.array(g, np.float32, copy=True))
         present = [w for w in work if w is not None]
-        if totals is not None:
-            sumsq, found = totals[0], bool(totals[1]) and bool(self.scaler)
-        elif present:
-            sumsq = total_sumsq(present)
         norm = None
-        if self.max_norm is not None and (present or totals is not None):
-            if sumsq is None:
-                if norm_override is None:
-                    raise ValueError("an unverified norm needs norm_override")
-            else:
-                norm = norm_from_sumsq(sumsq)
+        if self.max_norm is not None and present:
+            norm = norm_from_sumsq(total_sumsq(present))
             coef = clip_coef(norm if norm_override is None else norm_override, self.max_norm)
             for w in present:
                 scale_parallel(w, coef)
@@ -427,6 +489,41 @@ class OracleRun:
                 self.steps[i] += 1.0
                 adamw_parallel(self.p[i], work[i], self.m[i], self.v[i], lrs[self.group_of[i]], h["betas"][0],
                                h["betas"][1], h["eps"], h["weight_decay"], self.steps[i], h.get("maximize", False))
+        return self._finish(norm, found, skipped)
+
+    def _step_from_totals(self, grads, lrs, subset, norm_override, totals) -> dict:
+        """step() given the totals over every gradient: the found flag and the
+        clip coefficient are known before any tensor is touched, so each
+        tensor of the subset is unscaled, clipped and updated in one pass
+        (unscale_clip_adamw, bit for bit the separate steps), the tensors in
+        parallel."""
+        sumsq, found = totals[0], bool(totals[1]) and bool(self.scaler)
+        inv = inv_scale(self.scale) if self.scaler else 1.0
+        norm, coef = None, None
+        if self.max_norm is not None:
+            if sumsq is None:
+                if norm_override is None:
+                    raise ValueError("an unverified norm needs norm_override")
+            else:
+                norm = norm_from_sumsq(sumsq)
+            coef = clip_coef(norm if norm_override is None else norm_override, self.max_norm)
+        skipped = bool(self.scaler) and found
+        if not skipped:
+            jobs = []
+            for i in (range(len(self.p)) if subset is None else subset):
+                if grads[i] is None:
+                    continue
+                h = self.hparams[self.group_of[i]]
+                self.steps[i] += 1.0
+                kw = dict(inv=inv, unscale=bool(self.scaler), coef=coef, lr=lrs[self.group_of[i]],
+                          beta1=h["betas"][0], beta2=h["betas"][1], eps=h["eps"], wd=h["weight_decay"],
+                          step=self.steps[i], maximize=h.get("maximize", False))
+                g = np.ascontiguousarray(grads[i], np.float32).reshape(-1)
+                jobs.append((g, self.p[i], self.m[i], self.v[i], kw))
+            unscale_clip_adamw_many(jobs)
+        return self._finish(norm, found, skipped)
+
+    def _finish(self, norm, found, skipped) -> dict:
         out = {"norm": norm, "found_inf": found, "skipped": skipped}
         if self.scaler:
             out["scale_before"] = self.scale

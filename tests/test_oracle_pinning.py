@@ -313,3 +313,65 @@ def test_parallel_pieces_are_the_serial_arithmetic():
         O.adamw_parallel(s2[0], g, s2[1], s2[2], 1e-3, 0.9, 0.95, 1e-8, 0.1, step)
     for x, y in zip(s1, s2):
         assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("unscale,clip,maximize,wd", [(True, True, False, 0.1), (False, True, False, 0.0),
+                                                      (True, False, True, 0.1), (False, False, False, 0.1)])
+def test_fused_tensor_step_is_the_three_separate_steps(unscale, clip, maximize, wd):
+    """unscale_clip_adamw (one pass per tensor, used when the totals over all
+    gradients are known in advance) against unscale(), scale_() and adamw()
+    in turn: same bits for p, m and v over three steps, on a length that is
+    no multiple of its internal block and with zeros, subnormals, huge
+    values and a NaN among the gradients; and unscale_clip_adamw_many's
+    pieces equal one call."""
+    rng = np.random.default_rng(11)
+    n = 3 * 2048 + 77
+    g = (rng.standard_normal(n) * 3e2).astype(np.float32)
+    g[:5] = [0.0, -0.0, 1e-42, -3e38, np.nan]
+    inv, coef = np.float32(1 / 1024.0), np.float32(0.0173)
+    p0 = rng.standard_normal(n).astype(np.float32)
+    ref = [p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)]
+    got = [x.copy() for x in ref]
+    many = [x.copy() for x in ref]
+    for step in (1, 2, 3):
+        u = O.unscale(g, inv)[0] if unscale else g.copy()
+        if clip:
+            O.scale_(u, coef)
+        O.adamw(ref[0], u, ref[1], ref[2], 3e-4, 0.9, 0.95, 1e-8, wd, step, maximize)
+        O.unscale_clip_adamw(g, got[0], got[1], got[2], inv, unscale, coef if clip else None, 3e-4, 0.9, 0.95, 1e-8,
+                             wd, step, maximize)
+        kw = dict(inv=inv, unscale=unscale, coef=coef if clip else None, lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8,
+                  wd=wd, step=step, maximize=maximize)
+        O.unscale_clip_adamw_many([(g, many[0], many[1], many[2], kw)], piece=1000)
+    for a, b, c in zip(ref, got, many):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+
+
+def test_oracle_step_given_totals_matches_the_plain_step():
+    """OracleRun.step with the totals over every gradient given (the
+    full-size tests' form: fused per-tensor update, tensors in parallel) and
+    without (unscale, norm, clip and AdamW as separate passes): same norms,
+    skip decisions, scales and bits over 12 steps with an inf at step 5."""
+    rng = np.random.default_rng(5)
+    sizes = [5000, 1, 300, 70000, 4097]
+    init = [rng.standard_normal(n).astype(np.float32) * 0.02 for n in sizes]
+    hp = [dict(betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1), dict(betas=(0.8, 0.99), eps=1e-7, weight_decay=0.0)]
+    sc = dict(init_scale=1024.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=3)
+    group_of = [0, 1, 0, 0, 1]
+    a = O.OracleRun(init, group_of, hp, scaler=sc, max_norm=1.0)
+    b = O.OracleRun(init, group_of, hp, scaler=sc, max_norm=1.0)
+    for s in range(1, 13):
+        grads = [(rng.standard_normal(n) * 0.3 * a.scale).astype(np.float32) for n in sizes]
+        if s == 5:
+            grads[3][9] = np.inf
+        oa = a.step(grads, 1e-3)
+        tot = O.grads_sumsq([(g, "f32") for g in grads], inv=O.inv_scale(b.scale), unscale=True)
+        ob = b.step(grads, 1e-3, totals=tot)
+        assert oa["skipped"] == ob["skipped"] == (s == 5)
+        assert oa["scale"] == ob["scale"] and oa["tracker"] == ob["tracker"]
+        assert oa["norm"] == ob["norm"] or (math.isinf(oa["norm"]) and math.isinf(ob["norm"]))
+    for i in range(len(sizes)):
+        assert a.steps[i] == b.steps[i] == 11
+        for x, y in ((a.p[i], b.p[i]), (a.m[i], b.m[i]), (a.v[i], b.v[i])):
+            assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
