@@ -85,9 +85,10 @@ def _u16(a: np.ndarray):
 
 
 # --------------------------------------------------------------- conversions
-def to_bf16(x: np.ndarray) -> np.ndarray:
+def to_bf16(x: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
+    """bf16 bit patterns of x (round to nearest even), into `out` when given."""
     x = np.ascontiguousarray(x, dtype=np.float32)
-    out = np.empty(x.shape, np.uint16)
+    out = np.empty(x.shape, np.uint16) if out is None else out.reshape(x.shape)
     lib().orc_f32_to_bf16_array(_fp(x), _u16(out), x.size)
     return out
 
@@ -99,9 +100,10 @@ def from_bf16(h: np.ndarray) -> np.ndarray:
     return out
 
 
-def to_f16(x: np.ndarray) -> np.ndarray:
+def to_f16(x: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
+    """fp16 bit patterns of x (round to nearest even), into `out` when given."""
     x = np.ascontiguousarray(x, dtype=np.float32)
-    out = np.empty(x.shape, np.uint16)
+    out = np.empty(x.shape, np.uint16) if out is None else out.reshape(x.shape)
     lib().orc_f32_to_f16_array(_fp(x), _u16(out), x.size)
     return out
 

@@ -36,6 +36,9 @@ def exact_fraction(a: np.ndarray, b: np.ndarray) -> float:
     return float(np.mean(a.view(np.uint32) == b.view(np.uint32))) if a.dtype == np.float32 else float(np.mean(a == b))
 
 
+CHUNK = 1 << 24      # elements per piece of the comparisons below (bounds their temporaries)
+
+
 def ulp16(a_bits: np.ndarray, b_bits: np.ndarray) -> int:
     """Largest distance in units in the last place between two arrays of
     bf16/fp16 bit patterns (sign-magnitude mapped to a monotone integer line)."""
@@ -43,9 +46,21 @@ def ulp16(a_bits: np.ndarray, b_bits: np.ndarray) -> int:
         h = np.asarray(h, np.int64) & 0xFFFF
         return np.where(h & 0x8000, -(h & 0x7FFF), h)
 
-    if np.size(a_bits) == 0:
-        return 0
-    return int(np.max(np.abs(line(a_bits) - line(b_bits))))
+    a_bits, b_bits = np.asarray(a_bits).ravel(), np.asarray(b_bits).ravel()
+    worst = 0
+    for s in range(0, a_bits.size, CHUNK):
+        worst = max(worst, int(np.max(np.abs(line(a_bits[s:s + CHUNK]) - line(b_bits[s:s + CHUNK])))))
+    return worst
+
+
+def bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
+    """Whether two float32 arrays hold the same bit patterns everywhere
+    (NaN payloads included), compared piece by piece."""
+    a, b = np.asarray(a).ravel(), np.asarray(b).ravel()
+    if a.size != b.size:
+        return False
+    ua, ub = a.view(np.uint32), b.view(np.uint32)
+    return all(np.array_equal(ua[s:s + CHUNK], ub[s:s + CHUNK]) for s in range(0, ua.size, CHUNK))
 
 
 def rel(a: float, b: float) -> float:

@@ -13,13 +13,14 @@ from __future__ import annotations
 
 import importlib
 import math
+import time
 from dataclasses import dataclass, field
 
 import numpy as np
 import torch
 
 from oracle import oracle as O
-from tests._compare import RTOL_NORM, RTOL_STATE, ULP_LOWP, exact_fraction, maxrel, rel, ulp16
+from tests._compare import RTOL_NORM, RTOL_STATE, ULP_LOWP, bits_equal, exact_fraction, maxrel, rel, ulp16
 from tests._live import live
 
 mg = importlib.import_module("minigpt-train-infra_amd")
@@ -67,13 +68,58 @@ class Case:
     chunk_elems: int | None = None
     # Full-size mode: the oracle rebuilds the gradients it needs on the host
     # from the generator the GPU fill uses (bit-identical), instead of copying
-    # them back; the total norm over every gradient is rebuilt at the steps in
-    # verify_norm (None: every step), and at the other steps the oracle forms
-    # its clip coefficient from the GPU's norm (the subset's update still runs
-    # in the oracle's own arithmetic).
+    # them back.  Every step's total norm and non-finite flag are recomputed
+    # from the device gradients by torch in fp64 (device_totals) and, at the
+    # steps in verify_norm (None: every step), also rebuilt on the host; the
+    # GPU's norm must agree with them to RTOL_NORM before the oracle clips with
+    # it.  rotate: besides the subset tracked from the start, every other
+    # tensor is checked once per run, at one step: its state is copied from the
+    # GPU before that step, stepped by the oracle, and compared bit for bit
+    # after it.
     host_grads: bool = False
     verify_norm: set | None = None
+    rotate: bool = False
     arena: bool = False                           # gradients are views of the optimizer's gradient arena
+
+
+class HostStage:
+    """Host arrays reused across steps for device-to-host copies and rebuilt
+    gradients, one per key, grown when a larger one is asked for (the
+    full-size tests move gigabytes per step; fresh arrays would spend most of
+    that time faulting in pages)."""
+
+    def __init__(self):
+        self.arrays: dict = {}
+
+    def array(self, key, n: int, dtype=np.float32) -> np.ndarray:
+        a = self.arrays.get(key)
+        if a is None or a.size < n or a.dtype != np.dtype(dtype):
+            a = np.empty(max(n, 1), dtype)
+            self.arrays[key] = a
+        return a[:n]
+
+    def fetch(self, key, t: torch.Tensor) -> np.ndarray:
+        """A copy of device tensor t (fp32 as float32, 16-bit types as their
+        uint16 bit patterns) in the array for key."""
+        flat = t.detach().reshape(-1)
+        if flat.dtype != torch.float32:
+            flat = flat.view(torch.int16)
+        a = self.array(key, flat.numel(), np.float32 if flat.dtype == torch.float32 else np.int16)
+        torch.from_numpy(a).copy_(flat)
+        return a if a.dtype == np.float32 else a.view(np.uint16)
+
+
+def rotation_schedule(sizes: dict[int, int], steps: list[int]) -> dict[int, list[int]]:
+    """Assigns each tensor (index -> element count) to one of `steps`, largest
+    first onto the step with the fewest elements so far, so that every tensor
+    is checked once and the per-step host work is even."""
+    load = {s: 0 for s in steps}
+    plan: dict[int, list[int]] = {s: [] for s in steps}
+    for i in sorted(sizes, key=lambda k: (-sizes[k], k)):
+        s = min(steps, key=lambda k: (load[k], k))
+        plan[s].append(i)
+        load[s] += sizes[i]
+    return {s: sorted(v) for s, v in plan.items() if v}
 
 
 class Pair:
@@ -134,6 +180,22 @@ class Pair:
         self.norms_gpu: list[torch.Tensor] = []
         self.outs: list[dict] = []
         self.scale_gpu: list[torch.Tensor] = []
+        self.stage = HostStage()
+        self.rotation: dict[int, list[int]] = {}
+        if case.rotate:
+            tracked = set(keep)
+            bad = {s for s, inj in case.inject.items() if any(not math.isfinite(v) for (_, _, v) in inj)}
+            sizes = {i: (int(np.prod(sh)) if sh else 1) for i, (_, sh) in enumerate(self.shapes) if i not in tracked}
+            # from step 2: before the first step no state exists to copy
+            self.rotation = rotation_schedule(sizes, [s for s in range(2, case.steps + 1) if s not in bad])
+        self.norm_checks = {"steps": 0, "device_exact": 0, "host": 0, "host_exact": 0}
+        self.rotated_checked = 0
+        self.seconds: dict[str, float] = {}     # wall time of the full-size mode's phases
+
+    def _timed(self, phase: str, t0: float) -> float:
+        t = time.perf_counter()
+        self.seconds[phase] = self.seconds.get(phase, 0.0) + t - t0
+        return t
 
     def current_grads(self) -> list[torch.Tensor]:
         return self.grads if self.separate else [p.grad for p in self.params]
@@ -163,14 +225,14 @@ class Pair:
         if c.scaler:
             self.scale_gpu.append(self.scaler._scale.clone())
 
-    def host_synth_grad(self, step: int, i: int) -> np.ndarray:
+    def host_synth_grad(self, step: int, i: int, out: np.ndarray | None = None) -> np.ndarray:
         """Gradient i of iteration `step` as the GPU holds it (fp32 values),
-        injections included, rebuilt on the host."""
+        injections included, rebuilt on the host (into `out` when given)."""
         c = self.case
         scale = self.orc.scale if c.scaler else 1.0
         n = int(np.prod(self.shapes[i][1])) if self.shapes[i][1] else 1
         g = O.synth_grad(n, syn.GRAD_SEED, syn.grad_stream(step, i), O.synth_k(c.sigma * scale), self.grad_dtype(),
-                         c.tail[0], c.tail[1])
+                         c.tail[0], c.tail[1], out=out)
         for (ti, idx, val) in c.inject.get(step, []):
             if ti == i:
                 g[idx] = O.round_to(np.array([val], np.float32), self.grad_dtype())[0]
@@ -195,24 +257,96 @@ class Pair:
                                unscale=bool(c.scaler))
         return s1 + s2, f1 or f2
 
-    def oracle_step_host(self, step: int, lr: float) -> dict:
-        """The oracle's iteration from host-rebuilt gradients (host_grads mode;
-        runs after the GPU step, whose norm it may need)."""
+    def device_totals(self, inv: float, piece: int = 1 << 26) -> tuple[float, bool]:
+        """(sum of squares after the unscale, non-finite flag) over every
+        gradient the GPU holds, computed by torch on the device in fp64: each
+        element widened to fp32, multiplied by inv in fp32 when the scaler is
+        on (the unscale), then squared and summed in fp64 -- none of this
+        engine's kernels take part.  Pieces of at most `piece` elements bound
+        the temporaries."""
+        c = self.case
+        grads = self.current_grads()
+        dev = grads[0].device
+        total = torch.zeros((), dtype=torch.float64, device=dev)
+        bad = torch.zeros((), dtype=torch.bool, device=dev)
+        with torch.no_grad():
+            for g in grads:
+                flat = g.detach().reshape(-1)
+                for s in range(0, flat.numel(), piece):
+                    x = flat[s: s + piece]
+                    bad |= ~torch.isfinite(x).all()
+                    u = x.float()
+                    if c.scaler:
+                        u = u * inv
+                    d = u.double()
+                    total += torch.dot(d, d)
+        return float(total), bool(bad)
+
+    def snapshot(self, idx: list[int]) -> None:
+        """Copies the GPU state of tensors idx (fp32 parameter or master,
+        exp_avg, exp_avg_sq, step count) to the host and hands it to the
+        oracle, before the step that checks them (copies wait for the GPU)."""
+        t = time.perf_counter()
+        for slot, i in enumerate(idx):
+            st = self.opt.state[self.params[i]]
+            p = st["master_param"] if "master_param" in st else self.params[i]
+            arrays = [self.stage.fetch(("snap", slot, k), t) for k, t in
+                      (("p", p), ("m", st["exp_avg"]), ("v", st["exp_avg_sq"]))]
+            self.orc.load(i, *arrays, float(st["step"]))
+        self._timed("snapshots", t)
+
+    def check_rotated(self, idx: list[int], label: str, step: int) -> None:
+        """The GPU state of tensors idx after `step` against the oracle's step
+        from their snapshot, bit for bit (the bf16/fp16 model copy within
+        ULP_LOWP of the oracle's rounding); then the oracle forgets them."""
+        self.check_tracked(idx, label, step)
+        for i in idx:
+            self.orc.unload(i)
+        self.rotated_checked += len(idx)
+
+    def oracle_step_full(self, step: int, lr: float, rotated: list[int] = ()) -> dict:
+        """The oracle's iteration in full-size mode, after the GPU step: the
+        norm and non-finite flag from the device gradients (device_totals)
+        and, at verify_norm steps, from the host rebuild, each checked against
+        the GPU's norm; then the tracked subset and the rotated tensors
+        stepped from host-rebuilt gradients, clipped with the GPU's norm once
+        it has passed those checks."""
         c = self.case
         inv = O.inv_scale(self.orc.scale) if c.scaler else 1.0
-        subset = range(len(self.shapes)) if c.subset is None else c.subset
-        grads = [None] * len(self.shapes)
-        for i in subset:
-            grads[i] = self.host_synth_grad(step, i)
-        verify = c.verify_norm is None or step in c.verify_norm
-        gpu_norm = float(self.norms_gpu[-1]) if c.max_norm is not None else None
-        if verify:
-            totals = self.host_totals(step, inv)
-            out = self.orc.step(grads, lr, subset=list(subset), totals=totals)
-        else:
-            found = any(not math.isfinite(v) for (_, _, v) in c.inject.get(step, []))
-            out = self.orc.step(grads, lr, subset=list(subset), totals=(None, found), norm_override=gpu_norm)
-        out["verified"] = verify
+        t = time.perf_counter()
+        ng = float(self.norms_gpu[-1]) if c.max_norm is not None else None
+        torch.cuda.synchronize()
+        t = self._timed("gpu step", t)
+        dev_sum, found = self.device_totals(inv)
+        t = self._timed("device totals", t)
+        nd = O.norm_from_sumsq(dev_sum)
+        self.norm_checks["steps"] += 1
+        if ng is not None:
+            _check_norm(ng, nd, ("device fp64", step))
+            self.norm_checks["device_exact"] += ng == nd or not math.isfinite(nd)
+        if c.verify_norm is None or step in c.verify_norm:
+            host_sum, host_found = self.host_totals(step, inv)
+            nh = O.norm_from_sumsq(host_sum)
+            assert host_found == found, (step, host_found, found)
+            if math.isfinite(host_sum):
+                assert rel(host_sum, dev_sum) <= 1e-12, (step, host_sum, dev_sum)
+            if ng is not None:
+                _check_norm(ng, nh, ("host rebuild", step))
+                self.norm_checks["host_exact"] += ng == nh or not math.isfinite(nh)
+            self.norm_checks["host"] += 1
+            t = self._timed("host totals", t)
+        tracked = list(range(len(self.shapes))) if c.subset is None else list(c.subset)
+        work = sorted(set(tracked) | set(rotated))
+        grads: list = [None] * len(self.shapes)
+        for i in work:
+            key = ("grad", i) if i in tracked else ("grad_rot", rotated.index(i))
+            n = int(np.prod(self.shapes[i][1])) if self.shapes[i][1] else 1
+            grads[i] = self.host_synth_grad(step, i, out=self.stage.array(key, n))
+        t = self._timed("host gradients", t)
+        out = self.orc.step(grads, lr, subset=work, totals=(dev_sum, found), norm_override=ng)
+        self._timed("oracle step", t)
+        out["verified"] = True
+        out["norm_gpu"] = ng
         self.outs.append(out)
         return out
 
@@ -237,8 +371,13 @@ class Pair:
             mg.set_optimizer_lr(self.opt, lr)
             self.fill_grads(s)
             if oracle and c.host_grads:
+                rot = self.rotation.get(s, [])
+                if rot:
+                    self.snapshot(rot)
                 self.gpu_step()
-                self.oracle_step_host(s, lr)
+                self.oracle_step_full(s, lr, rot)
+                if rot:
+                    self.check_rotated(rot, "run", s)
                 continue
             if oracle:
                 self.oracle_step(s, lr)
@@ -261,9 +400,37 @@ class Pair:
             out["p"] = p.detach().cpu().numpy().ravel()
         return out
 
-    def oracle_lowp_bits(self, i: int) -> np.ndarray:
+    def oracle_lowp_bits(self, i: int, out: np.ndarray | None = None) -> np.ndarray:
         x = self.orc.p[i].ravel()
-        return O.to_bf16(x) if self.case.param_dtype == "bf16" else O.to_f16(x)
+        return O.to_bf16(x, out) if self.case.param_dtype == "bf16" else O.to_f16(x, out)
+
+    def check_tracked(self, idx, label: str, step: int) -> None:
+        """Tracked tensors idx against the oracle's, bit for bit (the
+        bf16/fp16 model copy within ULP_LOWP of the oracle's rounding), through
+        the reused host arrays."""
+        t = time.perf_counter()
+        for i in idx:
+            st = self.opt.state[self.params[i]]
+            lowp = "master_param" in st
+            p = st["master_param"] if lowp else self.params[i]
+            assert float(st["step"]) == self.orc.steps[i], (label, step, i, float(st["step"]), self.orc.steps[i])
+            for k, t, ref in (("p", p, self.orc.p[i]), ("m", st["exp_avg"], self.orc.m[i]),
+                              ("v", st["exp_avg_sq"], self.orc.v[i])):
+                assert bits_equal(self.stage.fetch(("after", k), t), ref), (label, step, k, i)
+            if lowp:
+                bits = self.stage.fetch(("after", "lowp"), self.params[i])
+                ref = self.oracle_lowp_bits(i, self.stage.array(("after", "lowp_ref"), bits.size, np.uint16))
+                assert ulp16(bits, ref) <= ULP_LOWP, (label, step, i)
+        self._timed("state comparisons", t)
+
+
+def _check_norm(gpu: float, ref: float, what) -> None:
+    """The GPU's norm against an independent one: within RTOL_NORM when
+    finite, else the same non-finite value (NaN for NaN)."""
+    if math.isfinite(ref):
+        assert rel(gpu, ref) <= RTOL_NORM, (what, gpu, ref)
+    else:
+        assert (math.isnan(ref) and math.isnan(gpu)) or gpu == ref, (what, gpu, ref)
 
 
 def check_pair(pair: Pair, indices=None, expect_exact=True, label="", device_bc=0):
