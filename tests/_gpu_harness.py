@@ -286,14 +286,14 @@ class Pair:
         """Copies the GPU state of tensors idx (fp32 parameter or master,
         exp_avg, exp_avg_sq, step count) to the host and hands it to the
         oracle, before the step that checks them (copies wait for the GPU)."""
-        t = time.perf_counter()
+        clock = time.perf_counter()
         for slot, i in enumerate(idx):
             st = self.opt.state[self.params[i]]
             p = st["master_param"] if "master_param" in st else self.params[i]
             arrays = [self.stage.fetch(("snap", slot, k), t) for k, t in
                       (("p", p), ("m", st["exp_avg"]), ("v", st["exp_avg_sq"]))]
             self.orc.load(i, *arrays, float(st["step"]))
-        self._timed("snapshots", t)
+        self._timed("snapshots", clock)
 
     def check_rotated(self, idx: list[int], label: str, step: int) -> None:
         """The GPU state of tensors idx after `step` against the oracle's step
@@ -408,7 +408,7 @@ class Pair:
         """Tracked tensors idx against the oracle's, bit for bit (the
         bf16/fp16 model copy within ULP_LOWP of the oracle's rounding), through
         the reused host arrays."""
-        t = time.perf_counter()
+        clock = time.perf_counter()
         for i in idx:
             st = self.opt.state[self.params[i]]
             lowp = "master_param" in st
@@ -421,7 +421,7 @@ class Pair:
                 bits = self.stage.fetch(("after", "lowp"), self.params[i])
                 ref = self.oracle_lowp_bits(i, self.stage.array(("after", "lowp_ref"), bits.size, np.uint16))
                 assert ulp16(bits, ref) <= ULP_LOWP, (label, step, i)
-        self._timed("state comparisons", t)
+        self._timed("state comparisons", clock)
 
 
 def _check_norm(gpu: float, ref: float, what) -> None:
