@@ -85,11 +85,21 @@ def _u16(a: np.ndarray):
 
 
 # --------------------------------------------------------------- conversions
+def _convert(fn, x: np.ndarray, out: np.ndarray) -> None:
+    """fn(in, out, n) over x, in parallel pieces when x is large."""
+    fx, fo = x.reshape(-1), out.reshape(-1)
+    if fx.size <= PIECE:
+        fn(_fp(fx), _u16(fo), fx.size)
+        return
+    list(pool().map(lambda s: fn(_fp(fx[s:s + PIECE]), _u16(fo[s:s + PIECE]), min(PIECE, fx.size - s)),
+                    range(0, fx.size, PIECE)))
+
+
 def to_bf16(x: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
     """bf16 bit patterns of x (round to nearest even), into `out` when given."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty(x.shape, np.uint16) if out is None else out.reshape(x.shape)
-    lib().orc_f32_to_bf16_array(_fp(x), _u16(out), x.size)
+    _convert(lib().orc_f32_to_bf16_array, x, out)
     return out
 
 
@@ -104,7 +114,7 @@ def to_f16(x: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
     """fp16 bit patterns of x (round to nearest even), into `out` when given."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty(x.shape, np.uint16) if out is None else out.reshape(x.shape)
-    lib().orc_f32_to_f16_array(_fp(x), _u16(out), x.size)
+    _convert(lib().orc_f32_to_f16_array, x, out)
     return out
 
 

@@ -37,6 +37,21 @@ def exact_fraction(a: np.ndarray, b: np.ndarray) -> float:
 
 
 CHUNK = 1 << 24      # elements per piece of the comparisons below (bounds their temporaries)
+_POOL = None
+
+
+def _map(fn, n: int) -> list:
+    """fn(start) for the pieces of an n-element comparison, in threads (numpy
+    releases the GIL inside these loops) when there is more than one."""
+    global _POOL
+    starts = range(0, n, CHUNK)
+    if len(starts) <= 1:
+        return [fn(s) for s in starts]
+    if _POOL is None:
+        from concurrent.futures import ThreadPoolExecutor
+
+        _POOL = ThreadPoolExecutor(max_workers=16)
+    return list(_POOL.map(fn, starts))
 
 
 def ulp16(a_bits: np.ndarray, b_bits: np.ndarray) -> int:
@@ -47,10 +62,14 @@ def ulp16(a_bits: np.ndarray, b_bits: np.ndarray) -> int:
         return np.where(h & 0x8000, -(h & 0x7FFF), h)
 
     a_bits, b_bits = np.asarray(a_bits).ravel(), np.asarray(b_bits).ravel()
-    worst = 0
-    for s in range(0, a_bits.size, CHUNK):
-        worst = max(worst, int(np.max(np.abs(line(a_bits[s:s + CHUNK]) - line(b_bits[s:s + CHUNK])))))
-    return worst
+
+    def piece(s: int) -> int:
+        a, b = a_bits[s:s + CHUNK], b_bits[s:s + CHUNK]
+        if np.array_equal(a, b):
+            return 0
+        return int(np.max(np.abs(line(a) - line(b))))
+
+    return max(_map(piece, a_bits.size), default=0)
 
 
 def bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
@@ -60,7 +79,7 @@ def bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
     if a.size != b.size:
         return False
     ua, ub = a.view(np.uint32), b.view(np.uint32)
-    return all(np.array_equal(ua[s:s + CHUNK], ub[s:s + CHUNK]) for s in range(0, ua.size, CHUNK))
+    return all(_map(lambda s: np.array_equal(ua[s:s + CHUNK], ub[s:s + CHUNK]), ua.size))
 
 
 def rel(a: float, b: float) -> float:

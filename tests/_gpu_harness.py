@@ -89,24 +89,33 @@ class HostStage:
     that time faulting in pages)."""
 
     def __init__(self):
-        self.arrays: dict = {}
+        self.buffers: dict = {}       # key -> page-locked host tensor
+
+    def _buffer(self, key, n: int, dtype: torch.dtype) -> torch.Tensor:
+        b = self.buffers.get(key)
+        if b is None or b.numel() < n or b.dtype != dtype:
+            self.buffers.pop(key, None)
+            b = torch.empty(max(n, 1), dtype=dtype, pin_memory=True)
+            self.buffers[key] = b
+        return b[:n]
 
     def array(self, key, n: int, dtype=np.float32) -> np.ndarray:
-        a = self.arrays.get(key)
-        if a is None or a.size < n or a.dtype != np.dtype(dtype):
-            a = np.empty(max(n, 1), dtype)
-            self.arrays[key] = a
-        return a[:n]
+        """A reused array of n elements in page-locked host memory (float32,
+        or uint16 bit patterns)."""
+        if np.dtype(dtype) == np.float32:
+            return self._buffer(key, n, torch.float32).numpy()
+        return self._buffer(key, n, torch.int16).numpy().view(np.uint16)
 
     def fetch(self, key, t: torch.Tensor) -> np.ndarray:
         """A copy of device tensor t (fp32 as float32, 16-bit types as their
-        uint16 bit patterns) in the array for key."""
+        uint16 bit patterns) in the array for key; page-locked, so the copy
+        runs at the link's speed."""
         flat = t.detach().reshape(-1)
         if flat.dtype != torch.float32:
             flat = flat.view(torch.int16)
-        a = self.array(key, flat.numel(), np.float32 if flat.dtype == torch.float32 else np.int16)
-        torch.from_numpy(a).copy_(flat)
-        return a if a.dtype == np.float32 else a.view(np.uint16)
+        b = self._buffer(key, flat.numel(), flat.dtype)
+        b.copy_(flat)
+        return b.numpy() if flat.dtype == torch.float32 else b.numpy().view(np.uint16)
 
 
 def rotation_schedule(sizes: dict[int, int], steps: list[int]) -> dict[int, list[int]]:

@@ -37,8 +37,10 @@ from tests._gpu_harness import log, mg
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
-#: parameter bar against torch's GPU AdamW (max |a - b| / max |b| per tensor)
-PARAM_BAR = 1e-5
+#: parameter bars against torch's GPU AdamW (max |a - b| / max |b| per tensor),
+#: about 1.5-2x the differences measured on MI355X (each test's docstring)
+PARAM_BAR_TINY = 1.5e-6
+PARAM_BAR_ARENA = 3e-6
 
 
 @pytest.fixture(autouse=True, params=[True, False], ids=["three_kernels", "five_kernels"])
@@ -224,7 +226,10 @@ def _fc_inf(model):
 
 
 def test_training_loop_matches_torch_on_the_same_model():
-    """40 steps, cosine schedule, GradScaler growth every 10, an inf at step 13."""
+    """40 steps, cosine schedule, GradScaler growth every 10, an inf at step 13.
+    Measured against torch on MI355X: parameters 7.5e-7 to 7.8e-7 (bar
+    1.5e-6), losses 1.1e-7, norms 1.6e-7; every step bit-exact against the
+    oracle."""
     torch.manual_seed(0)
     ref_model = TinyLM().to(DEV)
     my_model = copy.deepcopy(ref_model)
@@ -244,7 +249,7 @@ def test_training_loop_matches_torch_on_the_same_model():
     log(f"[train loop] oracle: {check.steps_checked} steps bit-exact, norms bit-equal {check.norms_exact}; against "
         f"torch: worst rel loss {worst_loss:.2e} norm {worst_norm:.2e} param {worst_param:.2e}")
     assert check.steps_checked == 40
-    assert worst_loss <= 1e-6 and worst_norm <= 1e-6 and worst_param <= PARAM_BAR
+    assert worst_loss <= 1e-6 and worst_norm <= 1e-6 and worst_param <= PARAM_BAR_TINY
     assert my_opt._engine.device_bc_flag() == 0
 
 
@@ -252,7 +257,9 @@ def test_accumulation_in_place_zeroing_and_a_torch_scheduler():
     """The same loop with gradients accumulated over 4 micro-batches,
     zero_grad(set_to_none=False) (the .grad tensors persist and are zeroed in
     place, so the optimizer sees the same gradient storage every step) and
-    torch's LambdaLR driving the learning rate; same bars as above."""
+    torch's LambdaLR driving the learning rate.  Measured against torch on
+    MI355X: parameters 9.5e-7 to 9.8e-7 (bar 1.5e-6); every step bit-exact
+    against the oracle."""
     torch.manual_seed(2)
     ref_model = TinyLM().to(DEV)
     my_model = copy.deepcopy(ref_model)
@@ -276,7 +283,7 @@ def test_accumulation_in_place_zeroing_and_a_torch_scheduler():
     log(f"[accumulation loop] oracle: {check.steps_checked} steps bit-exact, norms bit-equal {check.norms_exact}; "
         f"against torch: worst rel loss {worst_loss:.2e} norm {worst_norm:.2e} param {worst_param:.2e}")
     assert check.steps_checked == 30
-    assert worst_loss <= 1e-6 and worst_norm <= 1e-6 and worst_param <= PARAM_BAR
+    assert worst_loss <= 1e-6 and worst_norm <= 1e-6 and worst_param <= PARAM_BAR_TINY
     assert my_opt._engine.device_bc_flag() == 0
 
 
@@ -289,7 +296,11 @@ def test_grad_arena_accumulation_matches_torch(set_to_none):
     against torch AdamW(fused=False, foreach=False) + GradScaler on a copy.
     torch never gives the unused parameters a gradient, so it never steps
     them and keeps no state for them: the arena must do the same under both
-    zero_grad modes.  Same bars as the loops above."""
+    zero_grad modes.  Every step is bit-exact against the oracle; against
+    torch, parameters measured 1.69e-6 on MI355X (bar 3e-6).  With both
+    sides clipped by the same norm and this engine's steps bit-exact, that
+    figure is torch's GPU AdamW rounding and what it does to the later
+    forward passes of this (larger) model."""
     from tests._minigpt import MiniGPT, batches
 
     torch.manual_seed(4)
@@ -341,5 +352,5 @@ def test_grad_arena_accumulation_matches_torch(set_to_none):
         f"{check.norms_exact}; against torch: worst rel loss {worst_loss:.2e} norm {worst_norm:.2e} param "
         f"{worst_param:.2e}; key-bias abs diff {worst_kbias:.2e}")
     assert check.steps_checked == 24
-    assert worst_loss <= 1e-6 and worst_norm <= 1e-6 and worst_param <= PARAM_BAR
+    assert worst_loss <= 1e-6 and worst_norm <= 1e-6 and worst_param <= PARAM_BAR_ARENA
     assert worst_kbias <= len(data) * 3e-3 * 1e-1      # far below one full-size update per step
