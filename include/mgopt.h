@@ -190,8 +190,13 @@ MGOPT_API int mgopt_plan_flags(mgopt_plan* plan, int* out);
 
 /* The gradient L2 norm of one contiguous gradient buffer of n elements (a
  * flat gradient arena), with the outputs, scaling and arithmetic of
- * mgopt_grad_norm, and bit-identical to mgopt_grad_norm on a plan holding that
- * buffer as its one tensor.  Allocates nothing: its
+ * mgopt_grad_norm.  It sums the same 131,072-element chunks in the same order
+ * as mgopt_grad_norm on a plan holding that buffer as its one tensor in the
+ * five-kernel form (a plan of more than 2,097,152 elements, or any plan made
+ * with MGOPT_FOLD=0 in the environment), and is bit-identical to it there; a
+ * plan of at most 2,097,152 elements runs the three-kernel form, whose
+ * 16,384-element chunks group the fp64 partial sums differently, so the two
+ * can differ in the last bits of the fp64 total.  Allocates nothing: its
  * partial sums live in a static 1 MiB device array that each GPU holds until
  * the process ends, so n is at most 8,589,934,592 (65,536 chunks of 131,072
  * elements; larger n returns MGOPT_E_LIMIT).  Runs on the current device.  Calls that overlap on
