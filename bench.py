@@ -61,6 +61,8 @@ def log(msg: str) -> None:
 # one launch per tensor: the 20,000-tensor set then takes a few hundred set-up
 # dispatches instead of 40,000.  The tensors stay separate allocations.
 MANY_TENSORS = 1000
+#: steps shorter than 1 ms carry the per-pass HIP events at one step in this many
+EVENT_SAMPLE = 16
 
 
 def fill_tensors(tensors: list[torch.Tensor], seed: int, stream_of, sigma: float) -> None:
@@ -380,13 +382,22 @@ def main() -> int:
 
         one_step(False)
         torch.cuda.synchronize()
+    # Steps of a millisecond or more carry the per-pass HIP events at every
+    # step.  Shorter ones (small sets, whose step is a few launches) carry them
+    # at every EVENT_SAMPLE-th step only: three event records cost about as
+    # much host time as the step itself there, and would be measured with it.
+    probe = time.perf_counter()
+    for _ in range(5):
+        one_step(False)
+    torch.cuda.synchronize()
+    every = 1 if (time.perf_counter() - probe) / 5 >= 1e-3 else EVENT_SAMPLE
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        one_step(True)
+    for k in range(args.steps):
+        one_step(k % every == 0)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     step_s = (t1 - t0) / args.steps
-    taken = args.steps + args.warmup + (1 if args.graph else 0)
+    taken = args.steps + args.warmup + 5 + (1 if args.graph else 0)
     skipped = int(round(taken - float(eng.steps.max())))
     if eng.device_bc_flag() != 0 or skipped != 0:
         log(f"bias corrections evaluated on the device: {eng.device_bc_flag()}, skipped {skipped}")
@@ -455,6 +466,7 @@ def main() -> int:
         "implementation_GBps": (bpp + grad_bytes) * n_params / step_s / 1e9,
         "skipped_steps": skipped,
         "passes_ms": {"graph_replay": adamw_ms} if args.graph else {"norm": norm_ms, "adamw": adamw_ms},
+        "pass_events_every": every,
         "roofline": {
             "bound": "hbm",
             "achieved": adamw_gbps,

@@ -151,6 +151,18 @@ def host():
     return _host
 
 
+_addresses: dict[str, int] = {}
+
+
+def entry_address(name: str) -> int:
+    """The address of one of the library's entry points (for the host helper,
+    which calls the per-step ones directly)."""
+    addr = _addresses.get(name)
+    if addr is None:
+        addr = _addresses[name] = ctypes.cast(getattr(lib(), name), ctypes.c_void_p).value
+    return addr
+
+
 def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = load_library().mgopt_last_error().decode(errors="replace")

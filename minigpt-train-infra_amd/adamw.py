@@ -500,9 +500,9 @@ class AdamW(torch.optim.Optimizer):
         if track_unused:
             for i, p in enumerate(eng.params):
                 self._arena_hooks.append(p.register_post_accumulate_grad_hook(_GradMark(present, i)))
-            eng.present = present
+            eng.set_present(present)
         else:
-            eng.present = None
+            eng.set_present(None)
         self._grad_arena = arena
         self._grad_views = views
         eng.reset_iteration()

@@ -92,9 +92,7 @@ class _Engine:
             if p.dtype not in (torch.float32, torch.float16, torch.bfloat16):
                 raise TypeError(f"unsupported parameter dtype {p.dtype}")
         self.device = dev
-        lib = N.lib()
-        # the two per-iteration entry points, bound once
-        self._grad_norm, self._adamw_step = lib.mgopt_grad_norm, lib.mgopt_adamw_step
+        N.lib()                              # a GPU is visible and the library is built
         self.chunk_elems = int(chunk_elems or DEFAULT_CHUNK)
         lowp = [p.dtype != torch.float32 for p in self.params]
         if master_weights is False and any(lowp):
@@ -125,6 +123,7 @@ class _Engine:
             self.coef = torch.ones((), dtype=torch.float32, device=dev)
             # log-window record: norm_last, norm_max (fp32), skipped, taken (uint32)
             self.window = torch.zeros(4, dtype=torch.float32, device=dev)
+        self.found_inf_ptr, self.coef_ptr = self.found_inf.data_ptr(), self.coef.data_ptr()
         self.master_synced = not self.has_master
 
         # views handed out through optimizer.state
@@ -163,6 +162,7 @@ class _Engine:
         self.bc_src: list[tuple] | None = None   # the hp_key the table was last checked against
         self.bc_table: torch.Tensor | None = None
         self.hp = None                       # GroupHparams array passed to mgopt_adamw_step
+        self.hp_addr = 0                     # its address
         self.hp_key: list[tuple] | None = None
         self.hp_raw: list[tuple] | None = None
         # capturable: the kernels read the group records from a fixed device
@@ -270,7 +270,10 @@ class _Engine:
         (once per iteration: the norm pass and the step share it)."""
         if self.prepared:
             return
-        self._prepare()
+        ps = self._param_set()
+        if self.plan is None or not ps.unchanged():
+            self._prepare()
+            ps.remember()
         self.prepared = True
 
     def clear_grads(self) -> None:
@@ -278,9 +281,21 @@ class _Engine:
         self._param_set().clear_grads()
 
     def _param_set(self):
+        """The native view of the parameters (and gradient source) that
+        gathers the gradient table and launches the per-step entry points."""
         if self.pset is None:
-            self.pset = N.host().ParamSet(self.params, [] if self.grad_source is None else self.grad_source)
+            ps = N.host().ParamSet(self.params, [] if self.grad_source is None else self.grad_source)
+            ps.bind(N.entry_address("mgopt_grad_norm"), N.entry_address("mgopt_adamw_step"))
+            ps.set_mask(0 if self.present is None else self.present.ctypes.data)
+            self.pset = ps
         return self.pset
+
+    def set_present(self, present: np.ndarray | None) -> None:
+        """The arena's gradient-presence record (kept by backward hooks), or
+        None when every arena gradient counts."""
+        self.present = present
+        if self.pset is not None:
+            self.pset.set_mask(0 if present is None else present.ctypes.data)
 
     def _prepare(self) -> None:
         ps = self._param_set()
@@ -360,27 +375,27 @@ class _Engine:
         if self.norm_done and self.clip_pending:
             raise RuntimeError("clip_grad_norm_ was already called for this optimizer step")
         self.prepare()
-        out = torch.empty((), dtype=torch.float32, device=self.device)
-        self._launch_norm(out, max_norm)
+        out = self._launch_norm(True, max_norm)
         self.norm_done = True
         self.clip_pending = max_norm is not None
         return out
 
-    def _launch_norm(self, norm_out: torch.Tensor | None, max_norm: float | None) -> None:
-        """max_norm None: no clipping requested, the coefficient is not written."""
+    def _launch_norm(self, want_norm: bool, max_norm: float | None) -> torch.Tensor | None:
+        """Pass 1 (+ finalize); returns a fresh norm tensor when want_norm.
+        max_norm None: no clipping requested, the coefficient is not written."""
         scale = self.scale_src
-        N.check(
-            self._grad_norm(
-                self.plan,
-                scale.data_ptr() if scale is not None else None,
-                float(max_norm) if max_norm is not None else 0.0,
-                norm_out.data_ptr() if norm_out is not None else None,
-                self.coef.data_ptr() if max_norm is not None else None,
-                self.found_inf.data_ptr() if scale is not None else None,
-                self._stream(),
-            ),
-            "mgopt_grad_norm",
+        out = self.pset.grad_norm(
+            self.plan,
+            scale.data_ptr() if scale is not None else 0,
+            float(max_norm) if max_norm is not None else 0.0,
+            want_norm,
+            self.coef_ptr if max_norm is not None else 0,
+            self.found_inf_ptr if scale is not None else 0,
+            self._stream(),
         )
+        if isinstance(out, int):
+            N.check(out, "mgopt_grad_norm")
+        return out
 
     def _ensure_bc(self) -> None:
         """(Re)builds the bias-correction table when the reachable step bound
@@ -441,7 +456,7 @@ class _Engine:
         skip_src = None
         if scale is not None:
             if not self.norm_done:
-                self._launch_norm(None, None)   # found_inf only, no clipping
+                self._launch_norm(False, None)   # found_inf only, no clipping
             skip_src = self.found_inf
         else:
             if grad_scale is not None:
@@ -453,7 +468,7 @@ class _Engine:
         if self.t_bound + 2 > self.bc_cap or self.bc_src is not self.hp_key:
             self._ensure_bc()
         flags = N.WRITEBACK_GRADS if writeback else 0
-        groups_arg = self.hp
+        groups_addr = self.hp_addr
         if self.capturable:
             if capturing:
                 if self.hp_dev_key is None:
@@ -461,18 +476,17 @@ class _Engine:
                 self.captured = True
             elif self.hp_dev_key != self.hp_key:
                 self.upload_hparams()
-            groups_arg = ctypes.c_void_p(self.hp_dev.data_ptr())
+            groups_addr = self.hp_dev.data_ptr()
             flags |= N.GROUPS_ON_DEVICE
-        N.check(
-            self._adamw_step(
-                self.plan, groups_arg, self.bc_table.data_ptr(), self.bc_cap,
-                scale.data_ptr() if scale is not None else None,
-                self.coef.data_ptr() if self.clip_pending else None,
-                skip_src.data_ptr() if skip_src is not None else None,
-                flags, self._stream(),
-            ),
-            "mgopt_adamw_step",
+        rc = self.pset.adamw_step(
+            self.plan, groups_addr, self.bc_table.data_ptr(), self.bc_cap,
+            scale.data_ptr() if scale is not None else 0,
+            self.coef_ptr if self.clip_pending else 0,
+            skip_src.data_ptr() if skip_src is not None else 0,
+            flags, self._stream(),
         )
+        if rc:
+            N.check(rc, "mgopt_adamw_step")
         self.reset_iteration()
 
     def read_hparams(self) -> None:
@@ -497,6 +511,7 @@ class _Engine:
             for d, (lr, wd, b1, b2, eps, maximize) in zip(hp, key):
                 d.lr, d.weight_decay, d.beta1, d.beta2, d.eps, d.maximize = lr, wd, b1, b2, eps, int(maximize)
             self.hp, self.hp_key = hp, key
+            self.hp_addr = ctypes.addressof(hp)
         self.hp_raw = None if any(isinstance(r[0], torch.Tensor) for r in raw) else raw
 
     def upload_hparams(self) -> None:

@@ -179,14 +179,14 @@ class GradScaler:
             if getattr(self, "_found_ptrs", None) != ptrs:
                 # the optimizers' found_inf tensors persist: the pointer array is rebuilt only when they change
                 self._found_ptrs, self._found_arr = ptrs, (ctypes.c_void_p * len(ptrs))(*ptrs)
-            N.check(
-                N.lib().mgopt_scaler_update(
-                    _scale.data_ptr(), _tracker.data_ptr(), self._found_arr, len(ptrs),
-                    float(self._growth_factor), float(self._backoff_factor), int(self._growth_interval),
-                    N.stream_handle(_scale.device),
-                ),
-                "mgopt_scaler_update",
-            )
+                self._found_addr = ctypes.addressof(self._found_arr)
+            # one native call: the launch through the entry point's address
+            rc = N.host().scaler_update(
+                N.entry_address("mgopt_scaler_update"), _scale.data_ptr(), _tracker.data_ptr(), self._found_addr,
+                len(ptrs), float(self._growth_factor), float(self._backoff_factor), int(self._growth_interval),
+                N.stream_handle(_scale.device))
+            if rc:
+                N.check(rc, "mgopt_scaler_update")
         self._iters = {}
 
     # ------------------------------------------------------------ accessors
@@ -268,7 +268,7 @@ class GradScaler:
                 "A GradScaler instance may only be pickled at the beginning "
                 "of an iteration, or at the end after scaler.update()."
             )
-        transient = ("_found_ptrs", "_found_arr")
+        transient = ("_found_ptrs", "_found_arr", "_found_addr")
         state = {k: v for k, v in self.__dict__.items() if k not in transient}
         if self._enabled:
             state.update(_init_scale=self.get_scale(), _init_growth_tracker=self._get_growth_tracker(),
