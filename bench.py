@@ -17,6 +17,7 @@ exp_avg_sq (131 GB resident), synthetic data.  Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import gc
 import importlib
 import json
 import math
@@ -267,6 +268,49 @@ def vs_torch(name: str, steps: int, warmup: int, dev: torch.device) -> dict:
     }
 
 
+def time_allocation_round(name: str, dev: torch.device, steps: int, warmup: int) -> dict:
+    """The workload built again from fresh allocations in this process (after
+    the previous round's memory went back to the driver), its two passes timed
+    with HIP events at every step, then released.  The same pass over the same
+    sizes can run at a different speed depending on which physical memory
+    backs its buffers; rounds in one process show that spread apart from the
+    kernel."""
+    spec, _, params, groups = build_workload(name, dev)
+    opt = mg.AdamW(groups, lr=3e-4, betas=(0.9, 0.95), eps=1e-8)
+    scaler = mg.GradScaler("cuda", init_scale=65536.0)
+    scaler.scale(torch.ones((), device=dev))
+    grads = [torch.empty(p.shape, dtype=DT[spec["grad"]], device=dev) for p in params]
+    fill_tensors(grads, syn.GRAD_SEED, lambda i: syn.grad_stream(1, i), 1e-3 * 65536.0)
+    if spec["grad"] == spec["param"]:
+        for p, g in zip(params, grads):
+            p.grad = g
+    else:
+        opt.set_grad_source(grads)
+    stream = torch.cuda.current_stream(dev)
+    spans = []
+    for k in range(warmup + steps):
+        mg.set_optimizer_lr(opt, 3e-4)
+        scaler.unscale_(opt)
+        a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        a.record(stream)
+        mg.clip_grad_norm_(params, 1.0)
+        b.record(stream)
+        scaler.step(opt)
+        c.record(stream)
+        scaler.update()
+        if k >= warmup:
+            spans.append((a, b, c))
+    torch.cuda.synchronize()
+    norm = sorted(a.elapsed_time(b) for a, b, _ in spans)
+    adamw = sorted(b.elapsed_time(c) for _, b, c in spans)
+    out = {"norm_ms": norm[len(norm) // 2], "adamw_ms": adamw[len(adamw) // 2], "adamw_ms_min": adamw[0],
+           "adamw_ms_max": adamw[-1]}
+    del opt, scaler, grads, params, groups
+    gc.collect()
+    torch.cuda.empty_cache()
+    return out
+
+
 def _workload_name(name: str) -> str:
     try:
         workload_spec(name)
@@ -295,10 +339,16 @@ def main() -> int:
                     help="after the timed steps, also time the runtime's own device-to-device copy "
                          "(hipMemcpyAsync, torch's copy_) of a GIB-gibibyte buffer and torch's fill of it "
                          "(writes only) in this process, and report pass 2's rate against the copy")
+    ap.add_argument("--alloc-rounds", type=int, default=0, metavar="R",
+                    help="after the benchmark line's measurement, release the workload and build it again from "
+                         "fresh allocations R times in this process, timing both passes in each round (the spread "
+                         "that physical placement alone causes); reported under alloc_rounds")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB fp32 device copy (reads 1 GiB, writes 1 GiB) three times, "
                          "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    if args.alloc_rounds and args.graph:
+        ap.error("--alloc-rounds times eager steps; it does not combine with --graph")
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the optimizer step here has no multi-GPU path (use --gpus 1)", file=sys.stderr)
         return 2
@@ -317,7 +367,7 @@ def main() -> int:
         print(json.dumps(vs_torch(args.workload, args.steps, args.warmup, dev)), flush=True)
         return 0
     spec, ordered, params, groups = build_workload(args.workload, dev)
-    n_params = sum(p.numel() for p in params)
+    n_params, n_tensors = sum(p.numel() for p in params), len(params)
     log(f"workload {args.workload}: {len(params)} tensors, {n_params:,} params ({spec['param']} params, {spec['grad']} grads)")
 
     init_scale = 65536.0
@@ -423,6 +473,19 @@ def main() -> int:
         log(f"fill of {args.copy_ceiling:g} GiB (writes only): {copy['fill']['ms']:.3f} ms = "
             f"{copy['fill']['GBps']:.0f} GB/s")
 
+    rounds = None
+    if args.alloc_rounds > 0:
+        first = {"norm_ms": norm_ms, "adamw_ms": adamw_ms}
+        del one_step, opt, scaler, eng, params, groups, ordered
+        ev.clear()
+        gc.collect()
+        torch.cuda.empty_cache()
+        rounds = [first]
+        for r in range(1, args.alloc_rounds + 1):
+            rounds.append(time_allocation_round(args.workload, dev, max(args.steps, 5), max(args.warmup, 2)))
+            log(f"allocation round {r}: norm pass {rounds[-1]['norm_ms']:.3f} ms, AdamW pass "
+                f"{rounds[-1]['adamw_ms']:.3f} ms")
+
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the reference's CPU step on a bounded sample ...")
@@ -449,7 +512,7 @@ def main() -> int:
         "data": "synthetic (seeded counter-hash generator; random-init parameters of the named shapes)",
         "config": {
             "workload": args.workload,
-            "tensors": len(params),
+            "tensors": n_tensors,
             "params": n_params,
             "param_dtype": spec["param"],
             "grad_dtype": spec["grad"],
@@ -480,6 +543,8 @@ def main() -> int:
     if copy is not None:
         copy["adamw_frac_of_copy"] = adamw_gbps / copy["GBps"]
         out["copy_ceiling"] = copy
+    if rounds is not None:
+        out["alloc_rounds"] = rounds
     print(json.dumps(out), flush=True)
     return 0
 
