@@ -62,7 +62,20 @@ extern "C" {
  *   numel          element count (> 0).
  *   group          index into the group hyper-parameter array.
  *   grad_dtype     MGOPT_F32, MGOPT_F16 or MGOPT_BF16.
- *   lowp_dtype     MGOPT_BF16, MGOPT_F16, or MGOPT_NONE when lowp_dev is NULL. */
+ *   lowp_dtype     MGOPT_BF16, MGOPT_F16, or MGOPT_NONE when lowp_dev is NULL.
+ *   row_elems      0: param_dev, exp_avg_dev and exp_avg_sq_dev each hold the
+ *                  numel values contiguously.  > 0: they hold them in rows of
+ *                  row_elems values (row_elems divides numel and is a multiple
+ *                  of the plan's chunk_elems), row r of exp_avg / exp_avg_sq at
+ *                  exp_avg_dev / exp_avg_sq_dev + r * state_pitch and row r of
+ *                  param_dev at param_dev + r * param_pitch (param_pitch =
+ *                  row_elems for a contiguous parameter).  This lets a caller
+ *                  place one tensor's master, exp_avg and exp_avg_sq rows side
+ *                  by side in memory, which keeps the update's reads and
+ *                  write-backs of a row in neighbouring DRAM rows; lowp_dev
+ *                  and the gradient are always contiguous.
+ *   param_pitch,
+ *   state_pitch    row strides in elements (>= row_elems) when row_elems > 0. */
 typedef struct mgopt_tensor_desc {
     float* param_dev;
     void* lowp_dev;
@@ -73,6 +86,9 @@ typedef struct mgopt_tensor_desc {
     int32_t grad_dtype;
     int32_t lowp_dtype;
     int32_t reserved;
+    int64_t row_elems;
+    int64_t param_pitch;
+    int64_t state_pitch;
 } mgopt_tensor_desc;
 
 /* Per-group AdamW hyper-parameters for one step, as host doubles (the values

@@ -50,6 +50,9 @@ class TensorDesc(ctypes.Structure):
         ("grad_dtype", ctypes.c_int32),
         ("lowp_dtype", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+        ("row_elems", ctypes.c_int64),
+        ("param_pitch", ctypes.c_int64),
+        ("state_pitch", ctypes.c_int64),
     ]
 
 

@@ -220,6 +220,13 @@ class AdamW(torch.optim.Optimizer):
         .grad during the step (the reference leaves them in .grad;
         train.py never reads them after the step, so this is off by default).
     chunk_elems: elements per pass-2 work-group (a multiple of 512).
+    state_layout: "rows" (default) keeps each parameter's fp32 master,
+        exp_avg and exp_avg_sq rows side by side in memory when its row
+        length (the smallest product of trailing dimensions that is a
+        multiple of chunk_elems, at most 16,384 elements) exists, which the
+        update streams measurably faster; optimizer.state[p] then holds
+        strided views of p's shape (non-contiguous).  "separate" keeps every
+        state tensor contiguous in its own arena.
 
     capturable=True (torch/optim/adam.py:163-176, 343-346): step() may be
     captured in a HIP graph (torch.cuda.graph) together with the scaler's
@@ -251,6 +258,7 @@ class AdamW(torch.optim.Optimizer):
         master_weights: bool | None = None,
         writeback_grads: bool = False,
         chunk_elems: int | None = None,
+        state_layout: str = "rows",
     ):
         if isinstance(lr, torch.Tensor) and lr.numel() != 1:
             raise ValueError("Tensor lr must be 1-element")
@@ -285,6 +293,9 @@ class AdamW(torch.optim.Optimizer):
         self._master_weights = master_weights
         self._writeback = bool(writeback_grads)
         self._chunk_elems = chunk_elems
+        if state_layout not in ("rows", "separate"):
+            raise ValueError(f"state_layout must be 'rows' or 'separate', got {state_layout!r}")
+        self._state_layout = state_layout
         self._engine: _Engine | None = None
         self._state_dirty = False
         self._installed: set[int] = set()
@@ -300,7 +311,8 @@ class AdamW(torch.optim.Optimizer):
                 raise RuntimeError("this optimizer has not stepped yet: run one step outside graph capture "
                                    "before capturing")
             capturable = bool(self.defaults.get("capturable")) or any(g.get("capturable") for g in self.param_groups)
-            self._engine = _Engine(self, self._master_weights, self._chunk_elems, capturable=capturable)
+            self._engine = _Engine(self, self._master_weights, self._chunk_elems, capturable=capturable,
+                                   state_layout=self._state_layout)
         return self._engine
 
     def _reconcile_state(self) -> None:
@@ -640,7 +652,8 @@ class AdamW(torch.optim.Optimizer):
         # travel with them, the device engine does not
         st = super().__getstate__()
         st["state"] = {k: dict(v) for k, v in self.state.items()}
-        st.update(_master_weights=self._master_weights, _writeback=self._writeback, _chunk_elems=self._chunk_elems)
+        st.update(_master_weights=self._master_weights, _writeback=self._writeback, _chunk_elems=self._chunk_elems,
+                  _state_layout=self._state_layout)
         return st
 
     def __setstate__(self, state: dict[str, Any]) -> None:
@@ -648,6 +661,7 @@ class AdamW(torch.optim.Optimizer):
         self.__dict__.setdefault("_master_weights", None)
         self.__dict__.setdefault("_writeback", False)
         self.__dict__.setdefault("_chunk_elems", None)
+        self.__dict__.setdefault("_state_layout", "rows")
         self._engine = None
         self._installed = set()
         tracked = _TrackedState(self)

@@ -130,8 +130,29 @@ struct DevTensor {
     float* v;
     int64_t numel;
     int32_t group;
-    int32_t pad;
+    uint32_t row_chunks;  // 0: param, m, v contiguous; else pass-2 chunks per row of row-laid-out storage
+    int64_t ppitch;       // row stride of param (elements), when row_chunks > 0
+    int64_t spitch;       // row stride of m and v (elements), when row_chunks > 0
 };
+
+// Where pass-2 chunk `index` (chunk_elems elements) of tensor T starts in
+// its fp32 param, m and v.  Row-laid-out storage keeps a tensor's master, m
+// and v rows side by side; a chunk never crosses a row (the row length is a
+// multiple of chunk_elems), so one division per chunk places it.
+struct ChunkPtrs {
+    float* p;
+    float* m;
+    float* v;
+};
+__device__ __forceinline__ ChunkPtrs chunk_ptrs(const DevTensor& T, uint32_t index, int64_t chunk_elems) {
+    if (T.row_chunks == 0) {
+        const int64_t s = static_cast<int64_t>(index) * chunk_elems;
+        return {T.param + s, T.m + s, T.v + s};
+    }
+    const uint32_t r = index / T.row_chunks;
+    const int64_t c0 = static_cast<int64_t>(index - r * T.row_chunks) * chunk_elems;
+    return {T.param + r * T.ppitch + c0, T.m + r * T.spitch + c0, T.v + r * T.spitch + c0};
+}
 
 struct Chunk {
     uint32_t tensor;
@@ -891,9 +912,10 @@ __device__ __forceinline__ void adamw_chunk(const AdamArgs& a, const Chunk ck, G
 
     const int64_t start = static_cast<int64_t>(ck.index) * a.chunk_elems;
     const int64_t len = min(a.chunk_elems, T.numel - start);
-    float* __restrict__ P = T.param + start;
-    float* __restrict__ M = T.m + start;
-    float* __restrict__ V = T.v + start;
+    const ChunkPtrs cp = chunk_ptrs(T, ck.index, a.chunk_elems);
+    float* __restrict__ P = cp.p;
+    float* __restrict__ M = cp.m;
+    float* __restrict__ V = cp.v;
     g += start;
     void* L = nullptr;
     if constexpr (LOWP != MGOPT_NONE) L = static_cast<uint16_t*>(T.lowp) + start;
@@ -957,9 +979,10 @@ __global__ void __launch_bounds__(kAdamBlock)
     GT* __restrict__ g = static_cast<GT*>(a.grads[ck.tensor]);
     const int64_t start = static_cast<int64_t>(ck.index) * a.chunk_elems;
     const int64_t len = min(a.chunk_elems, T.numel - start);
-    float* __restrict__ P = T.param + start;
-    float* __restrict__ M = T.m + start;
-    float* __restrict__ V = T.v + start;
+    const ChunkPtrs cp = chunk_ptrs(T, ck.index, a.chunk_elems);
+    float* __restrict__ P = cp.p;
+    float* __restrict__ M = cp.m;
+    float* __restrict__ V = cp.v;
     void* L = nullptr;
     if constexpr (LOWP != MGOPT_NONE) L = static_cast<uint16_t*>(T.lowp) + start;
     if (g != nullptr) g += start;
@@ -1079,7 +1102,7 @@ __global__ void __launch_bounds__(kBlock)
     const int64_t start = static_cast<int64_t>(ck.index) * chunk_elems;
     const int64_t len = min(chunk_elems, T.numel - start);
     const LT* l = static_cast<const LT*>(T.lowp) + start;
-    float* p = T.param + start;
+    float* p = chunk_ptrs(T, ck.index, chunk_elems).p;
     int64_t done = 0;
     if (aligned(l, sizeof(LT) * 4) && aligned(p, 16)) {
         const int64_t nvec = len / 4;
@@ -1311,7 +1334,7 @@ extern "C" {
 
 MGOPT_API const char* mgopt_last_error(void) { return g_last_error.c_str(); }
 
-MGOPT_API const char* mgopt_version(void) { return "mgopt 0.1 gfx950"; }
+MGOPT_API const char* mgopt_version(void) { return "mgopt 0.2 gfx950"; }
 
 MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensors, int32_t n_groups, float* steps_dev,
                                 int64_t chunk_elems, mgopt_plan** out) {
@@ -1345,7 +1368,19 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
         if (d.numel >= (int64_t(1) << 31) * chunk_elems)
             return fail(MGOPT_E_LIMIT, "tensor " + std::to_string(i) + ": too many chunks");
         const int32_t lowp = all ? d.lowp_dtype : MGOPT_NONE;
-        host_t[i] = DevTensor{d.param_dev, all ? d.lowp_dev : nullptr, d.exp_avg_dev, d.exp_avg_sq_dev, d.numel, d.group, 0};
+        uint32_t row_chunks = 0;
+        if (d.row_elems != 0) {
+            if (d.row_elems < 0 || d.row_elems % chunk_elems != 0 || d.numel % d.row_elems != 0 ||
+                d.param_pitch < d.row_elems || d.state_pitch < d.row_elems || !all)
+                return fail(MGOPT_E_INVALID, "tensor " + std::to_string(i) +
+                                                 ": row_elems must divide numel and be a multiple of chunk_elems, "
+                                                 "with pitches of at least row_elems, on a tensor with optimizer state");
+            if (d.row_elems / chunk_elems > 0xFFFFFFFFll)
+                return fail(MGOPT_E_LIMIT, "tensor " + std::to_string(i) + ": rows of too many chunks");
+            row_chunks = static_cast<uint32_t>(d.row_elems / chunk_elems);
+        }
+        host_t[i] = DevTensor{d.param_dev, all ? d.lowp_dev : nullptr, d.exp_avg_dev, d.exp_avg_sq_dev, d.numel, d.group,
+                              row_chunks, d.param_pitch, d.state_pitch};
         buckets[bucket_of(d.grad_dtype, lowp)].push_back(i);
     }
     if (grads_only && with_state) return fail(MGOPT_E_INVALID, "a plan is either grads-only or has optimizer state for every tensor");

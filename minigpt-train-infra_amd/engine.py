@@ -39,8 +39,44 @@ CAPTURE_BC_CAP = 1 << 16            # fixed table size of a capturable engine (g
 HP_SLOTS = 4                        # pinned host buffers for device hyper-parameter uploads
 
 
+ROW_MAX = 16384                     # longest row (elements) laid out with its master / m / v rows side by side
+
+
 def _align(n: int) -> int:
     return (n + ALIGN_ELEMS - 1) // ALIGN_ELEMS * ALIGN_ELEMS
+
+
+def row_length(shape, chunk_elems: int) -> int:
+    """Row length of a parameter's row-laid-out state: the smallest product of
+    its trailing dimensions that is a multiple of the pass-2 chunk, up to
+    ROW_MAX elements; 0 when there is none (its state then lives in the
+    separate arenas).  Placing a row's master, exp_avg and exp_avg_sq side by
+    side keeps the update's reads and write-backs of those rows in
+    neighbouring DRAM rows: measured on MI355X with rows of 1,024-8,192
+    elements, a pass-2-shaped stream over 4.3e9 elements ran at 6.57-6.61 TB/s
+    against 6.07-6.38 TB/s with the three arrays apart (the best of three
+    relative offsets)."""
+    u = 1
+    for d in reversed(tuple(shape)):
+        u *= int(d)
+        if u > ROW_MAX:
+            return 0
+        if u % chunk_elems == 0:
+            return u
+    return 0
+
+
+def row_view(arena: torch.Tensor, offset: int, shape, row: int, fields: int) -> torch.Tensor:
+    """The view with `shape` of a tensor whose consecutive rows of `row`
+    elements lie fields * row elements apart in `arena`, from `offset`: the
+    trailing dimensions that make up a row keep their contiguous strides, the
+    leading ones step over the other fields' rows."""
+    shape = tuple(int(d) for d in shape)
+    strides, acc = [], 1
+    for d in reversed(shape):
+        strides.append(acc if acc < row else acc * fields)
+        acc *= d
+    return arena.as_strided(shape, tuple(reversed(strides)), offset)
 
 
 def bias_correction_table(beta1: float, beta2: float, cap: int, start: int = 0) -> list[float]:
@@ -63,7 +99,7 @@ def bias_correction_table(beta1: float, beta2: float, cap: int, start: int = 0) 
 
 class _Engine:
     def __init__(self, optimizer: torch.optim.Optimizer, master_weights: bool | None, chunk_elems: int | None,
-                 capturable: bool = False):
+                 capturable: bool = False, state_layout: str = "rows"):
         # weak: the optimizer owns the engine, and a reference cycle would hold
         # the arenas (up to 100+ GB) until the cyclic collector happens to run
         self._opt_ref = weakref.ref(optimizer)
@@ -99,25 +135,37 @@ class _Engine:
             raise ValueError("bf16/fp16 parameters need master_weights (fp32 master copy); master_weights=False is not supported")
         self.has_master = any(lowp)
 
-        # arena layout
+        # per-parameter segments on 256-byte boundaries (the layout of the
+        # gradient arena, AdamW.use_grad_arena)
         self.offsets: list[int] = []
         total = 0
         for p in self.params:
             self.offsets.append(total)
             total += _align(p.numel())
         self.total = total
+        # optimizer state: a parameter with a row length (row_length) keeps its
+        # master, exp_avg and exp_avg_sq rows side by side in the rows arena;
+        # the others keep each in its own arena, one contiguous segment each
+        self.rows = [row_length(p.shape, self.chunk_elems) if state_layout == "rows" else 0 for p in self.params]
+        self.fields = [3 if lp else 2 for lp in lowp]        # fp32 arrays per row-laid-out parameter
+        self.state_offsets: list[int] = []      # into exp_avg / exp_avg_sq (separate) or rows (row-laid-out)
         self.master_offsets: list[int | None] = []
-        mtotal = 0
-        for p, lp in zip(self.params, lowp):
-            if lp:
-                self.master_offsets.append(mtotal)
-                mtotal += _align(p.numel())
-            else:
+        stotal = mtotal = rtotal = 0
+        for p, lp, row, k in zip(self.params, lowp, self.rows, self.fields):
+            if row:
+                self.state_offsets.append(rtotal)
                 self.master_offsets.append(None)
+                rtotal += _align(k * p.numel())
+                continue
+            self.state_offsets.append(stotal)
+            stotal += _align(p.numel())
+            self.master_offsets.append(mtotal if lp else None)
+            mtotal += _align(p.numel()) if lp else 0
         with torch.cuda.device(dev):
-            self.exp_avg = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
-            self.exp_avg_sq = torch.zeros(max(total, 1), dtype=torch.float32, device=dev)
-            self.master = torch.empty(max(mtotal, 1), dtype=torch.float32, device=dev) if self.has_master else None
+            self.exp_avg = torch.zeros(max(stotal, 1), dtype=torch.float32, device=dev)
+            self.exp_avg_sq = torch.zeros(max(stotal, 1), dtype=torch.float32, device=dev)
+            self.master = torch.empty(max(mtotal, 1), dtype=torch.float32, device=dev) if mtotal else None
+            self.rows_arena = torch.zeros(max(rtotal, 1), dtype=torch.float32, device=dev) if rtotal else None
             self.steps = torch.zeros(len(self.params), dtype=torch.float32, device=dev)
             self.found_inf = torch.zeros((), dtype=torch.float32, device=dev)
             self.coef = torch.ones((), dtype=torch.float32, device=dev)
@@ -128,16 +176,20 @@ class _Engine:
 
         # views handed out through optimizer.state
         self.views: list[dict[str, torch.Tensor]] = []
-        for i, p in enumerate(self.params):
-            off, n = self.offsets[i], p.numel()
-            v = {
-                "step": self.steps[i],
-                "exp_avg": self.exp_avg[off : off + n].view(p.shape),
-                "exp_avg_sq": self.exp_avg_sq[off : off + n].view(p.shape),
-            }
-            mo = self.master_offsets[i]
-            if mo is not None:
-                v["master_param"] = self.master[mo : mo + n].view(p.shape)
+        for i, (p, lp) in enumerate(zip(self.params, lowp)):
+            off, n, row = self.state_offsets[i], p.numel(), self.rows[i]
+            v = {"step": self.steps[i]}
+            if row:
+                k = self.fields[i]
+                names = (["master_param"] if lp else []) + ["exp_avg", "exp_avg_sq"]
+                for f, name in enumerate(names):
+                    v[name] = row_view(self.rows_arena, off + f * row, p.shape, row, k)
+            else:
+                v["exp_avg"] = self.exp_avg[off : off + n].view(p.shape)
+                v["exp_avg_sq"] = self.exp_avg_sq[off : off + n].view(p.shape)
+                mo = self.master_offsets[i]
+                if mo is not None:
+                    v["master_param"] = self.master[mo : mo + n].view(p.shape)
             self.views.append(v)
 
         self.param_ptr_bytes = np.array([p.data_ptr() for p in self.params], np.int64).tobytes()
@@ -218,21 +270,26 @@ class _Engine:
         descs = (N.TensorDesc * len(self.params))()
         for i, p in enumerate(self.params):
             d = descs[i]
-            off = self.offsets[i]
-            mo = self.master_offsets[i]
-            if mo is None:
+            v = self.views[i]
+            if "master_param" not in v:
                 d.param_dev = p.data_ptr()
                 d.lowp_dev = None
                 d.lowp_dtype = N.NONE
             else:
-                d.param_dev = self.master.data_ptr() + 4 * mo
+                d.param_dev = v["master_param"].data_ptr()
                 d.lowp_dev = p.data_ptr()
                 d.lowp_dtype = N.dtype_code(p.dtype)
-            d.exp_avg_dev = self.exp_avg.data_ptr() + 4 * off
-            d.exp_avg_sq_dev = self.exp_avg_sq.data_ptr() + 4 * off
+            d.exp_avg_dev = v["exp_avg"].data_ptr()
+            d.exp_avg_sq_dev = v["exp_avg_sq"].data_ptr()
             d.numel = p.numel()
             d.group = self.group_index[i]
             d.grad_dtype = grad_dtypes[i]
+            row = self.rows[i]
+            if row:
+                pitch = self.fields[i] * row
+                d.row_elems = row
+                d.state_pitch = pitch
+                d.param_pitch = pitch if "master_param" in v else row
         plan = ctypes.c_void_p()
         with torch.cuda.device(self.device):
             N.check(

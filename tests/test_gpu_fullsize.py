@@ -35,12 +35,16 @@ from tests._gpu_harness import Case, Pair, log, mg, syn
 pytestmark = pytest.mark.gpu
 
 
-def _checksums(pair: Pair) -> list[int]:
+def _checksums(pair: Pair, piece: int = 1 << 28) -> list[int]:
+    """Integer sums of the bit patterns of every optimizer arena and every
+    parameter, summed in pieces (the int64 widening of one whole 98 GB arena
+    would not fit beside the set)."""
     eng = pair.opt._engine
-    arenas = [eng.exp_avg, eng.exp_avg_sq] + ([eng.master] if eng.master is not None else [])
-    if eng.master is None:
-        arenas += [p.detach() for p in pair.params]
-    return [int(a.reshape(-1).view(torch.int32).sum()) for a in arenas]
+    arenas = [a.reshape(-1).view(torch.int32) for a in (eng.exp_avg, eng.exp_avg_sq, eng.master, eng.rows_arena)
+              if a is not None]
+    arenas += [p.detach().reshape(-1).view(torch.int32 if p.dtype == torch.float32 else torch.int16)
+               for p in pair.params]
+    return [sum(int(a[s: s + piece].sum()) for s in range(0, a.numel(), piece)) for a in arenas]
 
 
 def _check_subset(pair: Pair, label: str, step: int) -> None:

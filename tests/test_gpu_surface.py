@@ -991,3 +991,72 @@ def test_model_copy_rounding_at_the_edges(dtype):
     assert torch.equal(torch.isnan(got.float()), nan)
     assert torch.equal(got.view(torch.int16)[~nan], want.view(torch.int16)[~nan])
     assert torch.equal(opt.state[p]["master_param"].cpu().view(torch.int32)[~nan], vals.view(torch.int32)[~nan])
+
+
+@pytest.mark.parametrize("pdt", [torch.bfloat16, torch.float32])
+def test_state_layouts_step_bit_identically_and_exchange_checkpoints(pdt, step_form):
+    """state_layout="rows" (each qualifying parameter's master / exp_avg /
+    exp_avg_sq rows side by side, strided views in optimizer.state) against
+    "separate" (contiguous arenas): shapes with and without a row length
+    (rows of 1,024 / 3,072 elements, a one-row vector, a 768-wide matrix
+    that keeps separate storage, a 3-D tensor whose row is its last two
+    dimensions), GradScaler with an inf at step 3, clip every step; 6 steps,
+    every state tensor and parameter bit-identical between the layouts.
+    Then each layout's state_dict, through torch.save / torch.load
+    (weights_only), loads into the other and the next step stays
+    bit-identical."""
+    shapes = [(5, 1024), (3072,), (2, 3072), (768, 768), (4, 2, 512), (7,), (1024, 3)]
+    mg_ = mg
+    opts, scalers, params = {}, {}, {}
+    for lay in ("rows", "separate"):
+        params[lay] = _params(shapes, pdt)
+        groups = [{"params": [p for p in params[lay] if p.dim() >= 2], "weight_decay": 0.1},
+                  {"params": [p for p in params[lay] if p.dim() < 2], "weight_decay": 0.0}]
+        opts[lay] = mg_.AdamW(groups, lr=1e-3, betas=(0.9, 0.95), eps=1e-8, state_layout=lay)
+        scalers[lay] = mg_.GradScaler("cuda", init_scale=1024.0, growth_interval=2)
+        scalers[lay].scale(torch.ones((), device=DEV))
+
+    def step(lay, s):
+        _grads(params[lay], s, 1e-2 * scalers[lay].get_scale())
+        if s == 3:
+            params[lay][2].grad.view(-1)[5] = float("inf")
+        scalers[lay].unscale_(opts[lay])
+        mg_.clip_grad_norm_(params[lay], 1.0)
+        scalers[lay].step(opts[lay])
+        scalers[lay].update()
+
+    def same():
+        torch.cuda.synchronize()
+        for pr, ps in zip(params["rows"], params["separate"]):
+            assert torch.equal(pr.detach(), ps.detach())
+            sr, ss = opts["rows"].state[pr], opts["separate"].state[ps]
+            assert set(sr) == set(ss)
+            for k in sr:
+                assert sr[k].shape == ss[k].shape and torch.equal(sr[k], ss[k]), k
+                if k != "step":
+                    assert ss[k].is_contiguous()
+
+    for s in range(1, 7):
+        for lay in ("rows", "separate"):
+            step(lay, s)
+    same()
+    eng = opts["rows"]._engine
+    rows = [mg_.engine.row_length(p.shape, eng.chunk_elems) for p in eng.params]
+    assert sorted(r for r in rows if r) == [1024, 1024, 3072, 3072, 3072] and rows.count(0) == 2
+    strided = [opts["rows"].state[p]["exp_avg"] for p, r in zip(eng.params, rows) if r and r < p.numel()]
+    assert strided and not any(t.is_contiguous() for t in strided)
+    assert opts["rows"].state[params["rows"][2]]["exp_avg_sq"].stride() == (3 * 3072 if pdt != torch.float32 else 2 * 3072, 1)
+
+    # checkpoints cross layouts
+    saved = {}
+    for lay in ("rows", "separate"):
+        buf = io.BytesIO()
+        torch.save(opts[lay].state_dict(), buf)
+        buf.seek(0)
+        saved[lay] = torch.load(buf, weights_only=True)
+    opts["rows"].load_state_dict(saved["separate"])
+    opts["separate"].load_state_dict(saved["rows"])
+    same()
+    for lay in ("rows", "separate"):
+        step(lay, 7)
+    same()

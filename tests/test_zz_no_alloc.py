@@ -34,7 +34,8 @@ class TensorDesc(ctypes.Structure):            # mgopt_tensor_desc
     _fields_ = [("param_dev", ctypes.c_void_p), ("lowp_dev", ctypes.c_void_p),
                 ("exp_avg_dev", ctypes.c_void_p), ("exp_avg_sq_dev", ctypes.c_void_p),
                 ("numel", ctypes.c_int64), ("group", ctypes.c_int32), ("grad_dtype", ctypes.c_int32),
-                ("lowp_dtype", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("lowp_dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("row_elems", ctypes.c_int64), ("param_pitch", ctypes.c_int64), ("state_pitch", ctypes.c_int64)]
 
 
 def _lib():
