@@ -122,10 +122,12 @@ MGOPT_API int64_t mgopt_plan_num_chunks(const mgopt_plan* plan);
 
 /* 1 when the plan runs a step as three kernels (a plan of at most 2,097,152
  * elements, no empty tensor, no tensor of more than 256 pass-2 chunks,
- * MGOPT_FOLD not "0" in the environment at creation): pass 1 finalizes in its last work-group and pass 2 forms the
- * step counts and constants itself; 0 for the five-kernel form (pass 1,
- * finalize, prologue, pass 2, scaler); -1 for NULL.  Both forms give the same
- * results.  No reference counterpart. */
+ * MGOPT_FOLD not "0" in the environment at creation; MGOPT_FOLD=1 lifts the
+ * two size limits for plans of up to 67,108,864 elements): pass 1 finalizes
+ * in its last work-group and pass 2 forms the step counts and constants
+ * itself; 0 for the five-kernel form (pass 1, finalize, prologue, pass 2,
+ * scaler); -1 for NULL.  Both forms give the same results.  No reference
+ * counterpart. */
 MGOPT_API int mgopt_plan_folded(const mgopt_plan* plan);
 
 /* Sets the gradient of every tensor for the coming step from a host array of

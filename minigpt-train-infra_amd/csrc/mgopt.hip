@@ -89,21 +89,21 @@ constexpr int64_t kNormChunk = 131072;
 // the scaler update.  A plan qualifies with at most kFoldElems elements, no
 // empty tensor and no tensor of more than kFoldTensorChunks pass-2 chunks:
 // every chunk of a tensor takes a ticket from that tensor's counter, one
-// counter per 128-byte line, and the atomics on one line serialize.  Measured
-// per step on MI355X against the five-kernel form (eager / replayed graph,
-// us): the 0.8M-parameter MiniGPT set (52 tensors) 21.5 / 20.0 against
-// 26.2 / 21.3; 0.26M elements in one tensor 19.1 / 19.1 against 23.7 / 23.5;
-// 1M in 16 tensors 19.9 / 20.7 against 24.8 / 21.9; 2M in 16 tensors
-// 23.1 / 27.3 against 27.5 / 31.2; 4M in 16 tensors 38.7 / 43.0 against
-// 38.4 / 42.1; one tensor of 1M elements (1,024 chunks on one counter)
-// 24.3 / 29.0 against 25.3 / 24.7.  Their
-// pass-1 chunks are shorter (4,096-16,384 measured the same).  MGOPT_FOLD=0
-// in the environment at plan creation keeps the five-kernel form.  (Folding
-// only the finalize into a pass 1 of one round of work-groups, GPT-2-small's
-// 950, measured 0.567 ms per step both ways: the ticket each work-group waits
-// for costs what the saved launch gains.)
+// counter per 128-byte line, and the atomics on one line serialize.  Beyond
+// these limits the saved launches no longer pay for the tickets: measured per
+// step on MI355X, the three-kernel form gains 2-6 us eager and 0.3-4 us as a
+// replayed graph on sets of up to 2M elements in tensors of at most 256
+// chunks, loses 2-9 us on 4M and 8M elements in 16 tensors, and 3.7 us
+// replayed on one tensor of 1,024 chunks.  Their pass-1 chunks are shorter
+// (4,096-16,384 measured the same).  MGOPT_FOLD=0 in the environment at plan
+// creation keeps the five-kernel form; MGOPT_FOLD=1 takes the three-kernel
+// form beyond the limits too, up to kFoldForcedElems (for measuring them).
+// (Folding only the finalize into a pass 1 of one round of work-groups,
+// GPT-2-small's 950, measured 0.567 ms per step both ways: the ticket each
+// work-group waits for costs what the saved launch gains.)
 constexpr int64_t kFoldElems = int64_t(1) << 21;
 constexpr int64_t kFoldTensorChunks = 256;
+constexpr int64_t kFoldForcedElems = int64_t(1) << 26;
 constexpr int64_t kNormChunkFold = 16384;
 constexpr uint32_t kTicketStride = 32;  // uint32 counters per 128-byte line: one tensor's ticket per line
 // A dispatch packet carries its grid size in work-items as a 32-bit value, so
@@ -1398,8 +1398,10 @@ MGOPT_API int mgopt_plan_create(const mgopt_tensor_desc* descs, int32_t n_tensor
         has_empty |= descs[i].numel == 0;
     }
     const char* fold_env = std::getenv("MGOPT_FOLD");
-    P->fold = total_elems > 0 && total_elems <= kFoldElems && !has_empty &&
-              (largest + chunk_elems - 1) / chunk_elems <= kFoldTensorChunks && !(fold_env && std::strcmp(fold_env, "0") == 0);
+    const bool fold_off = fold_env && std::strcmp(fold_env, "0") == 0;
+    const bool fold_forced = fold_env && std::strcmp(fold_env, "1") == 0;
+    const bool fold_fits = total_elems <= kFoldElems && (largest + chunk_elems - 1) / chunk_elems <= kFoldTensorChunks;
+    P->fold = total_elems > 0 && !has_empty && !fold_off && (fold_fits || (fold_forced && total_elems <= kFoldForcedElems));
     P->norm_chunk = P->fold ? kNormChunkFold : kNormChunk;
     P->n_tensors = n_tensors;
     P->n_groups = n_groups;

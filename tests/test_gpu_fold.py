@@ -145,3 +145,59 @@ def test_three_kernel_norms_match_the_oracle():
         want = O.norm_from_sumsq(O.total_sumsq([to_f32(*host_grad(g)) for g in grads]))
         assert norm == want or (np.isinf(norm) and np.isinf(want)), (n_tensors, size, norm, want)
         log(f"[fold norm] {n_tensors} x {size}: {norm!r} = oracle")
+
+
+def _forced_run(env: str, shapes, steps: int = 4):
+    saved = os.environ.get("MGOPT_FOLD")
+    os.environ["MGOPT_FOLD"] = env
+    try:
+        params = []
+        for i, s in enumerate(shapes):
+            p = torch.empty(s, dtype=torch.float32, device=DEV)
+            syn.fill_(p, syn.PARAM_SEED, syn.param_stream(i), 0.02)
+            params.append(torch.nn.Parameter(p))
+        opt = mg.AdamW(params, lr=1e-3, weight_decay=0.1)
+        grads = [torch.empty(s, dtype=torch.float16, device=DEV) for s in shapes]
+        opt.set_grad_source(grads)
+        sc = mg.GradScaler("cuda", init_scale=1024.0, growth_interval=2)
+        sc.scale(torch.ones((), device=DEV))
+        norms = []
+        for s in range(1, steps + 1):
+            for i, g in enumerate(grads):
+                syn.fill_(g, syn.GRAD_SEED, syn.grad_stream(s, i), 1e-2 * sc.get_scale())
+            if s == 2:
+                grads[0].view(-1)[-1] = float("nan")
+            sc.unscale_(opt)
+            norms.append(mg.clip_grad_norm_(params, 1.0).item())
+            sc.step(opt)
+            sc.update()
+        folded = opt._engine.folded()
+        torch.cuda.synchronize()
+        state = [[p.detach().clone(), opt.state[p]["exp_avg"].clone(), opt.state[p]["exp_avg_sq"].clone(),
+                  opt.state[p]["step"].clone()] for p in params]
+        return folded, norms, sc.get_scale(), state
+    finally:
+        if saved is None:
+            os.environ.pop("MGOPT_FOLD", None)
+        else:
+            os.environ["MGOPT_FOLD"] = saved
+
+
+@pytest.mark.parametrize("shapes", [[(1024, 300), (4099,)], [(1 << 20,), (1 << 20,), (70000,)]],
+                         ids=["300-chunk tensor", "2.16M elements"])
+def test_forced_three_kernel_step_beyond_the_limits(shapes):
+    """MGOPT_FOLD=1 takes the three-kernel form on plans the limits keep in the
+    five-kernel form (a tensor of more than 256 pass-2 chunks, more than
+    2,097,152 elements); 4 steps with a NaN step equal the five-kernel form's
+    bit for bit, norms included."""
+    log(f"case: forced three-kernel step, shapes {shapes}")
+    a = _forced_run("1", shapes)
+    b = _forced_run("0", shapes)
+    assert a[0] and not b[0]
+    assert a[1][1] != a[1][1] and b[1][1] != b[1][1]     # the NaN step's norm
+    assert a[1][0] == b[1][0] and a[1][2:] == b[1][2:] and a[2] == b[2]
+    for i, (ea, eb) in enumerate(zip(a[3], b[3])):
+        for k, (x, y) in enumerate(zip(ea, eb)):
+            assert np.array_equal(_bits(x), _bits(y)), (i, k)
+    assert float(a[3][0][3]) == 3.0
+    log(f"[forced fold] {shapes}: 4 steps equal bit for bit, norms {a[1]}")
