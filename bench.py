@@ -268,7 +268,8 @@ def vs_torch(name: str, steps: int, warmup: int, dev: torch.device) -> dict:
     }
 
 
-def time_allocation_round(name: str, dev: torch.device, steps: int, warmup: int, state_layout: str = "rows") -> dict:
+def time_allocation_round(name: str, dev: torch.device, steps: int, warmup: int, state_layout: str = "rows",
+                          chunk_elems: int | None = None) -> dict:
     """The workload built again from fresh allocations in this process (after
     the previous round's memory went back to the driver), its two passes timed
     with HIP events at every step, then released.  The same pass over the same
@@ -276,7 +277,7 @@ def time_allocation_round(name: str, dev: torch.device, steps: int, warmup: int,
     backs its buffers; rounds in one process show that spread apart from the
     kernel."""
     spec, _, params, groups = build_workload(name, dev)
-    opt = mg.AdamW(groups, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, state_layout=state_layout)
+    opt = mg.AdamW(groups, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, state_layout=state_layout, chunk_elems=chunk_elems)
     scaler = mg.GradScaler("cuda", init_scale=65536.0)
     scaler.scale(torch.ones((), device=dev))
     grads = [torch.empty(p.shape, dtype=DT[spec["grad"]], device=dev) for p in params]
@@ -342,6 +343,8 @@ def main() -> int:
     ap.add_argument("--state-layout", choices=("rows", "separate"), default="rows",
                     help="AdamW(state_layout=...): each parameter's master / exp_avg / exp_avg_sq rows side by side "
                          "(rows, the default) or each in its own contiguous arena (separate)")
+    ap.add_argument("--chunk-elems", type=int, default=None, metavar="N",
+                    help="AdamW(chunk_elems=N): elements per pass-2 work-group (a multiple of 512; default 1,024)")
     ap.add_argument("--alloc-rounds", type=int, default=0, metavar="R",
                     help="after the benchmark line's measurement, release the workload and build it again from "
                          "fresh allocations R times in this process, timing both passes in each round (the spread "
@@ -374,7 +377,8 @@ def main() -> int:
     log(f"workload {args.workload}: {len(params)} tensors, {n_params:,} params ({spec['param']} params, {spec['grad']} grads)")
 
     init_scale = 65536.0
-    opt = mg.AdamW(groups, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, capturable=args.graph, state_layout=args.state_layout)
+    opt = mg.AdamW(groups, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, capturable=args.graph, state_layout=args.state_layout,
+                   chunk_elems=args.chunk_elems)
     scaler = mg.GradScaler("cuda", init_scale=init_scale, growth_factor=2.0, backoff_factor=0.5, growth_interval=2000)
     scaler.scale(torch.ones((), device=dev))
     grads = [torch.empty(p.shape, dtype=DT[spec["grad"]], device=dev) for p in params]
@@ -486,7 +490,7 @@ def main() -> int:
         rounds = [first]
         for r in range(1, args.alloc_rounds + 1):
             rounds.append(time_allocation_round(args.workload, dev, max(args.steps, 5), max(args.warmup, 2),
-                                                args.state_layout))
+                                                args.state_layout, args.chunk_elems))
             log(f"allocation round {r}: norm pass {rounds[-1]['norm_ms']:.3f} ms, AdamW pass "
                 f"{rounds[-1]['adamw_ms']:.3f} ms")
 
@@ -521,7 +525,8 @@ def main() -> int:
             "param_dtype": spec["param"],
             "grad_dtype": spec["grad"],
             "state": ("fp32 master/exp_avg/exp_avg_sq" if spec["param"] != "f32" else "fp32 exp_avg/exp_avg_sq")
-                     + f", layout {args.state_layout}",
+                     + f", layout {args.state_layout}"
+                     + (f", pass-2 chunks of {args.chunk_elems}" if args.chunk_elems else ""),
             "step": "GradScaler.unscale_ + clip_grad_norm_(1.0) + AdamW + GradScaler.update"
                     + (", captured in one HIP graph and replayed (AdamW capturable=True)" if args.graph else ""),
             "parallelism": "single GPU",
