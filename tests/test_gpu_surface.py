@@ -768,22 +768,24 @@ def test_add_param_group_after_steps_matches_torch():
     assert opt._engine.device_bc_flag() == 0
 
 
-def test_add_param_group_keeps_bf16_masters_bit_exact():
+def test_add_param_group_keeps_bf16_masters_bit_exact(step_form):
     """With bf16 parameters the carried-over state includes the fp32 masters:
     adding a group after three steps equals, bit for bit, an optimizer built
-    with both groups whose late parameters had no gradients for those steps."""
-    shapes = [(64, 48), (48,), (33, 7), (91,)]
+    with both groups whose late parameters had no gradients for those steps.
+    Three of the tensors keep their state in the row layout (rows of 3,072 =
+    64 x 48, 2,048 and 1,024 elements), the others in the separate arenas."""
+    shapes = [(64, 48), (2, 2048), (48,), (33, 7), (3, 1024), (91,)]
 
     def make():
         return _params(shapes, torch.bfloat16)
 
     pa, pb = make(), make()
-    late = mg.AdamW([{"params": pa[:2], "weight_decay": 0.1}], lr=1e-3)
-    full = mg.AdamW([{"params": pb[:2], "weight_decay": 0.1}, {"params": pb[2:], "weight_decay": 0.0}], lr=1e-3)
+    late = mg.AdamW([{"params": pa[:3], "weight_decay": 0.1}], lr=1e-3)
+    full = mg.AdamW([{"params": pb[:3], "weight_decay": 0.1}, {"params": pb[3:], "weight_decay": 0.0}], lr=1e-3)
     for s in range(1, 7):
         if s == 4:
-            late.add_param_group({"params": pa[2:], "weight_decay": 0.0})
-        n = 2 if s < 4 else 4
+            late.add_param_group({"params": pa[3:], "weight_decay": 0.0})
+        n = 3 if s < 4 else 6
         _grads(pa[:n], s, 0.05)
         _grads(pb[:n], s, 0.05)
         for p in pb[n:]:
@@ -795,6 +797,8 @@ def test_add_param_group_keeps_bf16_masters_bit_exact():
         mg.clip_grad_norm_(pb[:n], 1.0)
         full.step()
     torch.cuda.synchronize()
+    assert late._engine.rows == full._engine.rows == [3072, 2048, 0, 0, 1024, 0]
+    assert not late.state[pa[1]]["exp_avg"].is_contiguous()
     for x, y in zip(pa, pb):
         assert torch.equal(x.view(torch.int16), y.view(torch.int16))
         for k in ("step", "exp_avg", "exp_avg_sq", "master_param"):
@@ -1060,3 +1064,39 @@ def test_state_layouts_step_bit_identically_and_exchange_checkpoints(pdt, step_f
     for lay in ("rows", "separate"):
         step(lay, 7)
     same()
+
+
+def test_sync_master_from_params_after_outside_writes(step_form):
+    """Parameters overwritten outside the optimizer (here: a bf16 copy of
+    other values) are read back into the fp32 masters by
+    sync_master_from_params(): every master equals its parameter widened to
+    fp32, in the row layout (rows of 2,048 and 1,024 elements) and in the
+    separate arenas, and the next step starts from them."""
+    shapes = [(2, 2048), (33, 7), (3, 1024), (91,)]
+    params = _params(shapes, torch.bfloat16)
+    opt = mg.AdamW(params, lr=1e-3, weight_decay=0.1)
+    for s in (1, 2):
+        _grads(params, s, 0.05)
+        opt.step()
+    with torch.no_grad():
+        for i, p in enumerate(params):
+            fresh = torch.empty(p.shape, dtype=torch.float32, device=DEV)
+            syn.fill_(fresh, syn.PARAM_SEED, syn.param_stream(100 + i), 0.5)
+            p.copy_(fresh)
+    opt.sync_master_from_params()
+    torch.cuda.synchronize()
+    assert opt._engine.rows == [2048, 0, 1024, 0]
+    for p in params:
+        assert torch.equal(opt.state[p]["master_param"], p.detach().float())
+    # the step after the sync updates from the re-read masters: with zeroed
+    # moments (written in place) and a zero gradient only the decoupled decay
+    # acts, p * float(1 - lr * wd)
+    for p in params:
+        opt.state[p]["exp_avg"].zero_()
+        opt.state[p]["exp_avg_sq"].zero_()
+        p.grad = torch.zeros_like(p)
+    before = [p.detach().float().clone() for p in params]
+    opt.step()
+    torch.cuda.synchronize()
+    for p, b in zip(params, before):
+        assert torch.equal(opt.state[p]["master_param"], b * torch.tensor(1 - 1e-3 * 0.1, dtype=torch.float32))
