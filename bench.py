@@ -41,7 +41,14 @@ HBM_PEAK_GBPS = 8000.0
 # compulsory bytes per parameter of one executed step, by (param dtype, grad dtype):
 # grad read + param (or master) read/write + exp_avg read/write + exp_avg_sq read/write
 # (+ the bf16/fp16 model-copy write when a master exists)
-BYTES_PER_PARAM = {("bf16", "bf16"): 28, ("f32", "f32"): 28, ("f32", "f16"): 26, ("f16", "f16"): 28}
+ELEM_BYTES = {"f32": 4, "f16": 2, "bf16": 2}
+
+
+def bytes_per_param(param: str, grad: str) -> int:
+    """Compulsory bytes per parameter of one executed step: the gradient
+    read, the fp32 param (or master), exp_avg and exp_avg_sq each read and
+    written, and the bf16/fp16 model copy written when a master exists."""
+    return ELEM_BYTES[grad] + 24 + (ELEM_BYTES[param] if param != "f32" else 0)
 DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
 
 WORKLOADS = {
@@ -85,10 +92,12 @@ def workload_spec(name: str) -> dict:
     return dict(param="f32", grad="f32")
 
 
-def build_workload(name: str, dev: torch.device, param_dtype: str | None = None):
+def build_workload(name: str, dev: torch.device, param_dtype: str | None = None, grad_dtype: str | None = None):
     spec = workload_spec(name)
     if param_dtype is not None:
-        spec["param"] = spec["grad"] = param_dtype
+        spec["param"] = param_dtype
+    if grad_dtype is not None:
+        spec["grad"] = grad_dtype
     shapes = mg.paramsets.shapes_of(name)
     decay = [(n, s) for n, s in shapes if len(s) >= 2]
     nodecay = [(n, s) for n, s in shapes if len(s) < 2]
@@ -211,7 +220,7 @@ def vs_torch(name: str, steps: int, warmup: int, dev: torch.device) -> dict:
     place); HIP events on the current stream bracket only the four calls.
     The two optimizers keep separate state and update the shared parameters
     in turn, each for warmup + steps iterations, twice."""
-    _, ordered, params, groups = build_workload(name, dev, param_dtype="f32")
+    _, ordered, params, groups = build_workload(name, dev, param_dtype="f32", grad_dtype="f32")
     n_params = sum(p.numel() for p in params)
     init_scale = 65536.0
     stream = torch.cuda.current_stream(dev)
@@ -269,14 +278,14 @@ def vs_torch(name: str, steps: int, warmup: int, dev: torch.device) -> dict:
 
 
 def time_allocation_round(name: str, dev: torch.device, steps: int, warmup: int, state_layout: str = "rows",
-                          chunk_elems: int | None = None) -> dict:
+                          chunk_elems: int | None = None, param_dtype: str | None = None) -> dict:
     """The workload built again from fresh allocations in this process (after
     the previous round's memory went back to the driver), its two passes timed
     with HIP events at every step, then released.  The same pass over the same
     sizes can run at a different speed depending on which physical memory
     backs its buffers; rounds in one process show that spread apart from the
     kernel."""
-    spec, _, params, groups = build_workload(name, dev)
+    spec, _, params, groups = build_workload(name, dev, param_dtype)
     opt = mg.AdamW(groups, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, state_layout=state_layout, chunk_elems=chunk_elems)
     scaler = mg.GradScaler("cuda", init_scale=65536.0)
     scaler.scale(torch.ones((), device=dev))
@@ -343,6 +352,9 @@ def main() -> int:
     ap.add_argument("--state-layout", choices=("rows", "separate"), default="rows",
                     help="AdamW(state_layout=...): each parameter's master / exp_avg / exp_avg_sq rows side by side "
                          "(rows, the default) or each in its own contiguous arena (separate)")
+    ap.add_argument("--param-dtype", choices=("bf16", "f16", "f32"), default=None,
+                    help="the workload's parameters in this dtype instead of its own (gradients keep theirs); "
+                         "bf16/fp16 parameters get fp32 masters")
     ap.add_argument("--chunk-elems", type=int, default=None, metavar="N",
                     help="AdamW(chunk_elems=N): elements per pass-2 work-group (a multiple of 512; default 1,024)")
     ap.add_argument("--alloc-rounds", type=int, default=0, metavar="R",
@@ -372,7 +384,7 @@ def main() -> int:
     if args.vs_torch:
         print(json.dumps(vs_torch(args.workload, args.steps, args.warmup, dev)), flush=True)
         return 0
-    spec, ordered, params, groups = build_workload(args.workload, dev)
+    spec, ordered, params, groups = build_workload(args.workload, dev, args.param_dtype)
     n_params, n_tensors = sum(p.numel() for p in params), len(params)
     log(f"workload {args.workload}: {len(params)} tensors, {n_params:,} params ({spec['param']} params, {spec['grad']} grads)")
 
@@ -463,7 +475,7 @@ def main() -> int:
     norm_ms = sum(a.elapsed_time(b) for a, b in ev["norm"]) / len(ev["norm"]) if ev["norm"] else 0.0
     adamw_ms = sum(a.elapsed_time(b) for a, b in ev["adamw"]) / len(ev["adamw"])
 
-    bpp = BYTES_PER_PARAM[(spec["param"], spec["grad"])]
+    bpp = bytes_per_param(spec["param"], spec["grad"])
     grad_bytes = 2 if spec["grad"] != "f32" else 4
     achieved_step = bpp * n_params / step_s / 1e9
     adamw_gbps = bpp * n_params / (adamw_ms * 1e-3) / 1e9
@@ -490,7 +502,7 @@ def main() -> int:
         rounds = [first]
         for r in range(1, args.alloc_rounds + 1):
             rounds.append(time_allocation_round(args.workload, dev, max(args.steps, 5), max(args.warmup, 2),
-                                                args.state_layout, args.chunk_elems))
+                                                args.state_layout, args.chunk_elems, args.param_dtype))
             log(f"allocation round {r}: norm pass {rounds[-1]['norm_ms']:.3f} ms, AdamW pass "
                 f"{rounds[-1]['adamw_ms']:.3f} ms")
 
