@@ -315,7 +315,7 @@ def adamw(p, g, m, v, lr, beta1, beta2, eps, wd, step, maximize=False) -> None:
 
 
 PIECE = 1 << 22          # elements per piece of the parallel element-wise helpers
-THREADS = 16             # threads of the parallel helpers (the GPU box's CPU share)
+THREADS = 16             # threads of the parallel helpers (the host cores available per GPU)
 _POOL = None
 
 
