@@ -30,7 +30,7 @@ import torch
 
 from oracle import oracle as O
 from tests._compare import RTOL_NORM, exact_fraction, rel
-from tests._gpu_harness import Case, Pair, log, mg, syn
+from tests._gpu_harness import Case, Pair, log, mg, rotation_schedule, syn
 
 pytestmark = pytest.mark.gpu
 
@@ -244,8 +244,11 @@ def test_ragged_20k_full_size_2000_steps():
     first bad step, every arena unchanged; at the end every step count, and
     60 tensors (the 20 largest, the 20 smallest and 20 in the middle) stepped
     by the oracle through all 2,000 steps from the same gradients, bit for
-    bit.  The scale climbs from 65536 to 2^30 and comes back down, so
-    clipping is active early and inactive late."""
+    bit; each of the other 19,940 tensors at one step of the run, from its
+    state copied off the GPU before that step, with the scale and the clip
+    coefficient of the host totals, bit for bit.  The scale climbs from 65536
+    to 2^30 and comes back down, so clipping is active early and inactive
+    late."""
     shapes = mg.paramsets.WORKLOADS["ragged_20k"]()
     rng = np.random.RandomState(11)
     bad_steps = sorted(rng.choice(np.arange(1, 2001), 20, replace=False).tolist())
@@ -263,27 +266,6 @@ def test_ragged_20k_full_size_2000_steps():
     k = O.synth_k(1e-2 * 65536)
     for i, g in enumerate(grads):
         syn.fill_(g, syn.GRAD_SEED, syn.grad_stream(1, i), 1e-2 * 65536)
-    injected = {}
-    for s in range(1, 2001):
-        restore = None
-        if s in bad_steps:
-            ti = int(rng.randint(len(grads)))
-            restore = (ti, grads[ti].view(-1)[0].clone())
-            injected[s] = (ti, float("nan") if s % 2 else float("inf"))
-            grads[ti].view(-1)[0] = injected[s][1]
-        before = _checksums(pair) if s == bad_steps[0] else None
-        mg.set_optimizer_lr(pair.opt, 1e-4)
-        pair.gpu_step()
-        if before is not None:
-            assert _checksums(pair) == before, "a skipped step changed the optimizer state"
-        if restore is not None:
-            grads[restore[0]].view(-1)[0] = restore[1]
-        if s % 500 == 0:
-            log(f"[ragged full] GPU step {s}")
-    torch.cuda.synchronize()
-    norms = torch.stack(pair.norms_gpu).cpu().numpy().tolist()
-    gpu_scales = torch.stack(pair.scale_gpu).cpu().numpy().tolist()
-    log("[ragged full] GPU 2000 steps done; host rebuild of every gradient")
 
     # every gradient as the GPU holds it, rebuilt on the host into one flat array
     offsets = np.concatenate([[0], np.cumsum(numel)])
@@ -313,8 +295,58 @@ def test_ragged_20k_full_size_2000_steps():
         totals[scale] = direct[0]
     for scale in distinct:
         totals.setdefault(scale, derived(scale))
-    log(f"[ragged full] host totals at {len(distinct)} distinct scales ({distinct[0]:g} .. {distinct[-1]:g}); "
-        f"oracle replay of the 60-tensor subset")
+    log(f"[ragged full] host gradients rebuilt; totals at {len(distinct)} distinct scales "
+        f"({distinct[0]:g} .. {distinct[-1]:g})")
+
+    # every tensor outside the tracked subset is checked at one step: its
+    # state copied from the GPU before that step, stepped by the oracle from
+    # the host gradient with the scale and the clip coefficient of the host
+    # totals (nothing taken from the GPU), compared bit for bit after it
+    rotation = rotation_schedule({i: numel[i] for i in range(len(numel)) if i not in set(subset)},
+                                 [s for s in range(2, 2001) if s not in bad_steps])
+
+    def rotated_step(idx: list[int], step: int) -> None:
+        sc_before = before_step[step - 1]
+        coef = O.clip_coef(O.norm_from_sumsq(totals[sc_before]), 1.0)
+        jobs = []
+        for i in idx:
+            h = pair.orc.hparams[pair.orc.group_of[i]]
+            pair.orc.steps[i] += 1.0
+            jobs.append((host[i], pair.orc.p[i], pair.orc.m[i], pair.orc.v[i],
+                         dict(inv=O.inv_scale(sc_before), unscale=True, coef=coef, lr=1e-4, beta1=h["betas"][0],
+                              beta2=h["betas"][1], eps=h["eps"], wd=h["weight_decay"], step=pair.orc.steps[i])))
+        O.unscale_clip_adamw_many(jobs)
+
+    injected = {}
+    for s in range(1, 2001):
+        restore = None
+        if s in bad_steps:
+            ti = int(rng.randint(len(grads)))
+            restore = (ti, grads[ti].view(-1)[0].clone())
+            injected[s] = (ti, float("nan") if s % 2 else float("inf"))
+            grads[ti].view(-1)[0] = injected[s][1]
+        before = _checksums(pair) if s == bad_steps[0] else None
+        rotated = rotation.get(s, [])
+        if rotated:
+            torch.cuda.synchronize()
+            pair.snapshot(rotated)
+        mg.set_optimizer_lr(pair.opt, 1e-4)
+        pair.gpu_step()
+        if before is not None:
+            assert _checksums(pair) == before, "a skipped step changed the optimizer state"
+        if rotated:
+            rotated_step(rotated, s)
+            torch.cuda.synchronize()
+            pair.check_rotated(rotated, "ragged full rotated", s)
+        if restore is not None:
+            grads[restore[0]].view(-1)[0] = restore[1]
+        if s % 500 == 0:
+            log(f"[ragged full] GPU step {s}; {pair.rotated_checked} rotated tensors bit-exact so far")
+    torch.cuda.synchronize()
+    norms = torch.stack(pair.norms_gpu).cpu().numpy().tolist()
+    gpu_scales = torch.stack(pair.scale_gpu).cpu().numpy().tolist()
+    assert pair.rotated_checked == len(numel) - len(subset)
+    log("[ragged full] GPU 2000 steps done; oracle replay of the 60-tensor subset")
 
     sub_grads = [host[i] if i in set(subset) else None for i in range(len(host))]
     exact_norms = 0
@@ -349,4 +381,6 @@ def test_ragged_20k_full_size_2000_steps():
     sizes = sorted((numel[i] for i in subset), reverse=True)
     log(f"[ragged full] final scale {gpu_scales[-1]}; {2000 - len(bad_steps)} norms checked against the host total "
         f"({exact_norms} bit-equal), {len(bad_steps)} skips; {clipped} steps clipped; {len(subset)} tensors "
-        f"(largest {sizes[0]}, smallest {sizes[-1]} elements) bit-exact after 2000 steps")
+        f"(largest {sizes[0]}, smallest {sizes[-1]} elements) bit-exact after 2000 steps; tensors value-checked: "
+        f"{len(subset)} tracked from step 1 + {pair.rotated_checked} rotated = {len(subset) + pair.rotated_checked} "
+        f"of {len(numel)}")
