@@ -22,7 +22,8 @@ from tests._gpu_harness import log, mg, syn
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
-SHAPES = [(64, 33), (1000,), (7,), (300, 5), (2, 131072)]
+# (4, 2048) keeps its state in the row layout (rows of 2,048 elements)
+SHAPES = [(64, 33), (1000,), (7,), (300, 5), (2, 131072), (4, 2048)]
 
 
 def _setup(capturable: bool, dtype=torch.float32):
@@ -97,6 +98,7 @@ def test_captured_step_replays_match_eager(dtype, fold, monkeypatch):
         _compare(pe, oe, se, pg, og, sg, norm_e, norm_g, f"eager step {s}")
 
     assert og._engine.folded() == oe._engine.folded() == fold
+    assert og._engine.rows == oe._engine.rows == [0, 0, 0, 2048, 0, 0]
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         norm_g = _eager_step(pg, og, sg)          # recorded, not run
