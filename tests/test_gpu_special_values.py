@@ -24,9 +24,10 @@ from tests._gpu_harness import Case, Pair, check_pair, log, mg
 
 pytestmark = pytest.mark.gpu
 
-# decay: w0, w1 (3 x 4099: chunks of 4096, 4096, 4096 and 9 elements), w2;
-# no decay: b0 (7), s (one element), b1 (4101: a vector body and a scalar tail)
-SHAPES = [("w0", (64, 130)), ("w1", (3, 4099)), ("w2", (4096, 2)), ("b0", (7,)), ("s", (1,)), ("b1", (4101,))]
+# decay: w0, w1 (3 x 4099: chunks of 4096, 4096, 4096 and 9 elements), w2 (2 x 4096:
+# state in the row layout, two rows); no decay: b0 (7), s (one element), b1 (4101: a
+# vector body and a scalar tail)
+SHAPES = [("w0", (64, 130)), ("w1", (3, 4099)), ("w2", (2, 4096)), ("b0", (7,)), ("s", (1,)), ("b1", (4101,))]
 CHUNK = 4096
 
 
@@ -62,6 +63,7 @@ def test_nonfinite_at_chunk_edges_and_tails():
     assert pair.outs[-1]["scale"] == 65536.0 / 64
     check_pair(pair, label="chunk_edges")
     assert all(float(pair.opt.state[p]["step"]) == 4.0 for p in pair.params)
+    assert pair.opt._engine.rows == [0, 0, 4096, 0, 0, 0]
 
 
 def test_norm_overflow_with_finite_gradients():
