@@ -1,7 +1,8 @@
 """GPU parity on 24 seeded random configurations against the oracle: parameter
 dtype (fp32, or bf16 / fp16 with an fp32 master), gradient dtype, tensor sizes
 (1 element to several 131,072-element pass-1 chunks, odd sizes for the scalar
-tails), chunk size, one or two groups with random betas (both lerp branches),
+tails; the 4,096- and 65,536-element tensors as matrices whose state takes the
+row layout), chunk size, one or two groups with random betas (both lerp branches),
 eps, weight decay and maximize, a GradScaler with a random initial scale and
 growth interval or none, clipping or none, and NaN / +inf / -inf injected at a
 random position on some steps.
@@ -33,6 +34,9 @@ from tests._gpu_harness import host_grad, log, mg, syn, to_f32
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+# matrices whose optimizer state takes the row layout at chunks of up to 4,096
+# (16 rows of 4,096 elements; 2 rows of 2,048 at chunks of 512 to 2,048)
+SHAPE_OF = {65536: (16, 4096), 4096: (2, 2048)}
 
 
 def _config(seed: int) -> dict:
@@ -73,7 +77,7 @@ def test_random_configuration_against_the_oracle(seed, monkeypatch):
         f"clip {c['max_norm']} bad {sorted(c['bad'])} at {c['bad_pos']:.3f}{' MGOPT_FOLD=0' if five else ''}")
     params = []
     for i, n in enumerate(c["sizes"]):
-        p = torch.empty(n, dtype=DT[c["pdt"]], device=DEV)
+        p = torch.empty(SHAPE_OF.get(n, (n,)), dtype=DT[c["pdt"]], device=DEV)
         syn.fill_(p, 3, 100 * seed + i, 0.05)
         params.append(torch.nn.Parameter(p))
     groups = []
