@@ -330,10 +330,11 @@ def test_torch_adamw_state_dict_loads_and_continues():
 def test_writes_into_state_entries_take_effect_as_in_torch():
     """Writing into a parameter's state entry changes the next step exactly as
     it does for torch's CPU AdamW: a step count reset to 0 and a zeroed
-    exp_avg on one tensor, a new exp_avg_sq on the other, after 3 steps; 3
+    exp_avg on one tensor, a new exp_avg_sq on the second, new exp_avg and
+    exp_avg_sq on a third whose state is in the row layout, after 3 steps; 3
     more steps then match torch to 1e-6.  state_dict() entries are plain
     dicts (torch.load(weights_only=True) accepts no other class)."""
-    shapes = [(40, 30), (30,)]
+    shapes = [(40, 30), (30,), (3, 1024)]
     init = [O.synth(int(np.prod(s)), 1, 10 + i, O.synth_k(0.02)).reshape(s) for i, s in enumerate(shapes)]
     cpu = [torch.nn.Parameter(torch.from_numpy(x.copy())) for x in init]
     gpu = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in cpu]
@@ -352,12 +353,19 @@ def test_writes_into_state_entries_take_effect_as_in_torch():
     for s in range(1, 4):
         step(s)
     new_v = O.synth(30, 5, 7, O.synth_k(1e-3)).reshape(30) ** 2
+    new_m2 = O.synth(3072, 5, 8, O.synth_k(1e-3)).reshape(3, 1024)
+    new_v2 = O.synth(3072, 5, 9, O.synth_k(1e-3)).reshape(3, 1024) ** 2
     topt.state[cpu[0]]["step"] = torch.tensor(0.0)
     topt.state[cpu[0]]["exp_avg"] = torch.zeros(40, 30)
     topt.state[cpu[1]]["exp_avg_sq"] = torch.from_numpy(new_v.copy())
+    topt.state[cpu[2]]["exp_avg"] = torch.from_numpy(new_m2.copy())
+    topt.state[cpu[2]]["exp_avg_sq"] = torch.from_numpy(new_v2.copy())
+    assert opt._engine.rows == [0, 0, 1024]
     opt.state[gpu[0]]["step"] = torch.tensor(0.0)
     opt.state[gpu[0]]["exp_avg"] = torch.zeros(40, 30, device=DEV)
     opt.state[gpu[1]]["exp_avg_sq"] = torch.from_numpy(new_v.copy()).to(DEV)
+    opt.state[gpu[2]]["exp_avg"] = torch.from_numpy(new_m2.copy()).to(DEV)
+    opt.state[gpu[2]]["exp_avg_sq"] = torch.from_numpy(new_v2.copy()).to(DEV)
     assert all(type(e) is dict for e in opt.state_dict()["state"].values())
     for s in range(4, 7):
         step(s)
@@ -368,6 +376,7 @@ def test_writes_into_state_entries_take_effect_as_in_torch():
         for k in ("exp_avg", "exp_avg_sq"):
             assert maxrel(opt.state[q][k].cpu().numpy(), topt.state[p][k].numpy()) <= RTOL_STATE, k
     assert float(opt.state[gpu[0]]["step"]) == 3.0 and float(opt.state[gpu[1]]["step"]) == 6.0
+    assert not opt.state[gpu[2]]["exp_avg"].is_contiguous()     # the row-layout view again
 
 
 def test_state_assigned_in_param_dtype_is_picked_up():
@@ -377,9 +386,10 @@ def test_state_assigned_in_param_dtype_is_picked_up():
     parameters the moments and the master arrive as bf16; the optimizer keeps
     them in its fp32 arenas from then on and continues exactly as the oracle
     does from the same rounded state."""
-    shapes = [("w", (96, 40)), ("c", (4097,)), ("b", (40,))]
+    shapes = [("w", (96, 40)), ("c", (4097,)), ("b", (40,)), ("r", (2, 2048))]
     pair = Pair(Case(shapes=shapes, param_dtype="bf16", grad_dtype="bf16", steps=8, sigma=1e-3, tail=(1000, 100.0)))
     pair.run(4)
+    assert pair.opt._engine.rows == [0, 2048, 0, 0]      # r (decay group, second) in the row layout
     saved = [{k: v.detach().cpu().clone() for k, v in pair.opt.state[p].items()} for p in pair.params]
     assert all(set(st) == {"step", "exp_avg", "exp_avg_sq", "master_param"} for st in saved)
     pair.opt.state.clear()
