@@ -219,7 +219,10 @@ class AdamW(torch.optim.Optimizer):
     writeback_grads: also store the unscaled, clipped gradient into each
         .grad during the step (the reference leaves them in .grad;
         train.py never reads them after the step, so this is off by default).
-    chunk_elems: elements per pass-2 work-group (a multiple of 512).
+    chunk_elems: elements per pass-2 work-group (a multiple of 512); by
+        default 2,048 for a set small enough for the three-kernel step at that
+        chunk (at most 2,097,152 elements, no tensor of more than 256 chunks),
+        1,024 otherwise.
     state_layout: "rows" (default) keeps each parameter's fp32 master,
         exp_avg and exp_avg_sq rows side by side in memory when its row
         length (the smallest product of trailing dimensions that is a

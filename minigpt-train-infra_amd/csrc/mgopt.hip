@@ -91,9 +91,9 @@ constexpr int64_t kNormChunk = 131072;
 // every chunk of a tensor takes a ticket from that tensor's counter, one
 // counter per 128-byte line, and the atomics on one line serialize.  Beyond
 // these limits the saved launches no longer pay for the tickets: measured per
-// step on MI355X, the three-kernel form gains 2-6 us eager and 0.3-4 us as a
+// step on MI355X, the three-kernel form gains 2-7 us eager and 1-5 us as a
 // replayed graph on sets of up to 2M elements in tensors of at most 256
-// chunks, loses 2-9 us on 4M and 8M elements in 16 tensors, and 3.7 us
+// chunks, loses 2-6 us on 4M and 8M elements in 16 tensors, and 3.9 us
 // replayed on one tensor of 1,024 chunks.  Their pass-1 chunks are shorter
 // (4,096-16,384 measured the same).  MGOPT_FOLD=0 in the environment at plan
 // creation keeps the five-kernel form; MGOPT_FOLD=1 takes the three-kernel

@@ -175,7 +175,7 @@ def _forced_run(env: str, shapes, steps: int = 4):
         torch.cuda.synchronize()
         state = [[p.detach().clone(), opt.state[p]["exp_avg"].clone(), opt.state[p]["exp_avg_sq"].clone(),
                   opt.state[p]["step"].clone()] for p in params]
-        return folded, norms, sc.get_scale(), state
+        return folded, norms, sc.get_scale(), state, opt._engine.chunk_elems
     finally:
         if saved is None:
             os.environ.pop("MGOPT_FOLD", None)
@@ -183,8 +183,8 @@ def _forced_run(env: str, shapes, steps: int = 4):
             os.environ["MGOPT_FOLD"] = saved
 
 
-@pytest.mark.parametrize("shapes", [[(1024, 300), (4099,)], [(1 << 20,), (1 << 20,), (70000,)]],
-                         ids=["300-chunk tensor", "2.16M elements"])
+@pytest.mark.parametrize("shapes", [[(2048, 300), (4099,)], [(1 << 20,), (1 << 20,), (70000,)]],
+                         ids=["600-chunk tensor", "2.16M elements"])
 def test_forced_three_kernel_step_beyond_the_limits(shapes):
     """MGOPT_FOLD=1 takes the three-kernel form on plans the limits keep in the
     five-kernel form (a tensor of more than 256 pass-2 chunks, more than
@@ -194,6 +194,7 @@ def test_forced_three_kernel_step_beyond_the_limits(shapes):
     a = _forced_run("1", shapes)
     b = _forced_run("0", shapes)
     assert a[0] and not b[0]
+    assert a[4] == b[4] == 1024      # beyond the limits the default chunk is 1,024 elements
     assert a[1][1] != a[1][1] and b[1][1] != b[1][1]     # the NaN step's norm
     assert a[1][0] == b[1][0] and a[1][2:] == b[1][2:] and a[2] == b[2]
     for i, (ea, eb) in enumerate(zip(a[3], b[3])):

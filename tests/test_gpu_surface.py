@@ -334,7 +334,7 @@ def test_writes_into_state_entries_take_effect_as_in_torch():
     exp_avg_sq on a third whose state is in the row layout, after 3 steps; 3
     more steps then match torch to 1e-6.  state_dict() entries are plain
     dicts (torch.load(weights_only=True) accepts no other class)."""
-    shapes = [(40, 30), (30,), (3, 1024)]
+    shapes = [(40, 30), (30,), (3, 2048)]
     init = [O.synth(int(np.prod(s)), 1, 10 + i, O.synth_k(0.02)).reshape(s) for i, s in enumerate(shapes)]
     cpu = [torch.nn.Parameter(torch.from_numpy(x.copy())) for x in init]
     gpu = [torch.nn.Parameter(p.detach().clone().to(DEV)) for p in cpu]
@@ -353,14 +353,14 @@ def test_writes_into_state_entries_take_effect_as_in_torch():
     for s in range(1, 4):
         step(s)
     new_v = O.synth(30, 5, 7, O.synth_k(1e-3)).reshape(30) ** 2
-    new_m2 = O.synth(3072, 5, 8, O.synth_k(1e-3)).reshape(3, 1024)
-    new_v2 = O.synth(3072, 5, 9, O.synth_k(1e-3)).reshape(3, 1024) ** 2
+    new_m2 = O.synth(6144, 5, 8, O.synth_k(1e-3)).reshape(3, 2048)
+    new_v2 = O.synth(6144, 5, 9, O.synth_k(1e-3)).reshape(3, 2048) ** 2
     topt.state[cpu[0]]["step"] = torch.tensor(0.0)
     topt.state[cpu[0]]["exp_avg"] = torch.zeros(40, 30)
     topt.state[cpu[1]]["exp_avg_sq"] = torch.from_numpy(new_v.copy())
     topt.state[cpu[2]]["exp_avg"] = torch.from_numpy(new_m2.copy())
     topt.state[cpu[2]]["exp_avg_sq"] = torch.from_numpy(new_v2.copy())
-    assert opt._engine.rows == [0, 0, 1024]
+    assert opt._engine.rows == [0, 0, 2048]
     opt.state[gpu[0]]["step"] = torch.tensor(0.0)
     opt.state[gpu[0]]["exp_avg"] = torch.zeros(40, 30, device=DEV)
     opt.state[gpu[1]]["exp_avg_sq"] = torch.from_numpy(new_v.copy()).to(DEV)
@@ -782,9 +782,10 @@ def test_add_param_group_keeps_bf16_masters_bit_exact(step_form):
     """With bf16 parameters the carried-over state includes the fp32 masters:
     adding a group after three steps equals, bit for bit, an optimizer built
     with both groups whose late parameters had no gradients for those steps.
-    Three of the tensors keep their state in the row layout (rows of 3,072 =
-    64 x 48, 2,048 and 1,024 elements), the others in the separate arenas."""
-    shapes = [(64, 48), (2, 2048), (48,), (33, 7), (3, 1024), (91,)]
+    Three of the tensors keep their state in the row layout (rows of 4,096 =
+    64 x 64 and of 2,048 elements at this small set's 2,048-element chunks),
+    the others in the separate arenas."""
+    shapes = [(64, 64), (2, 2048), (64,), (33, 7), (3, 2048), (91,)]
 
     def make():
         return _params(shapes, torch.bfloat16)
@@ -807,7 +808,8 @@ def test_add_param_group_keeps_bf16_masters_bit_exact(step_form):
         mg.clip_grad_norm_(pb[:n], 1.0)
         full.step()
     torch.cuda.synchronize()
-    assert late._engine.rows == full._engine.rows == [3072, 2048, 0, 0, 1024, 0]
+    assert late._engine.chunk_elems == full._engine.chunk_elems == 2048
+    assert late._engine.rows == full._engine.rows == [4096, 2048, 0, 0, 2048, 0]
     assert not late.state[pa[1]]["exp_avg"].is_contiguous()
     for x, y in zip(pa, pb):
         assert torch.equal(x.view(torch.int16), y.view(torch.int16))
@@ -1080,9 +1082,9 @@ def test_sync_master_from_params_after_outside_writes(step_form):
     """Parameters overwritten outside the optimizer (here: a bf16 copy of
     other values) are read back into the fp32 masters by
     sync_master_from_params(): every master equals its parameter widened to
-    fp32, in the row layout (rows of 2,048 and 1,024 elements) and in the
-    separate arenas, and the next step starts from them."""
-    shapes = [(2, 2048), (33, 7), (3, 1024), (91,)]
+    fp32, in the row layout (two and three rows of 2,048 elements) and in
+    the separate arenas, and the next step starts from them."""
+    shapes = [(2, 2048), (33, 7), (3, 2048), (91,)]
     params = _params(shapes, torch.bfloat16)
     opt = mg.AdamW(params, lr=1e-3, weight_decay=0.1)
     for s in (1, 2):
@@ -1095,7 +1097,7 @@ def test_sync_master_from_params_after_outside_writes(step_form):
             p.copy_(fresh)
     opt.sync_master_from_params()
     torch.cuda.synchronize()
-    assert opt._engine.rows == [2048, 0, 1024, 0]
+    assert opt._engine.rows == [2048, 0, 2048, 0]
     for p in params:
         assert torch.equal(opt.state[p]["master_param"], p.detach().float())
     # the step after the sync updates from the re-read masters: with zeroed

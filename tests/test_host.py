@@ -3,6 +3,7 @@
 from __future__ import annotations
 
 import ctypes
+import math
 import importlib
 import re
 from pathlib import Path
@@ -355,3 +356,28 @@ def test_state_dict_loads_with_weights_only(mg):
     buf.seek(0)
     back = torch.load(buf, weights_only=True)
     assert float(back["optimizer"]["state"][0]["step"]) == 2.0
+
+
+def test_row_lengths_and_the_default_chunk(mg):
+    """The row of a parameter's row-laid-out state is the smallest product of
+    its trailing dimensions that is a multiple of the pass-2 chunk, up to
+    16,384 elements; the default chunk is 2,048 elements exactly when the set
+    runs the three-kernel step at that chunk (at most 2,097,152 elements, no
+    empty tensor, no tensor of more than 256 chunks), else 1,024."""
+    eng = importlib.import_module("minigpt-train-infra_amd.engine")
+    assert eng.row_length((4096, 4096), 1024) == 4096
+    assert eng.row_length((4096, 12288), 1024) == 12288
+    assert eng.row_length((64, 48), 1024) == 3072 and eng.row_length((64, 48), 2048) == 0
+    assert eng.row_length((4, 2, 512), 1024) == 1024 and eng.row_length((4, 2, 512), 2048) == 4096
+    assert eng.row_length((768, 768), 1024) == 0 and eng.row_length((128,), 1024) == 0
+    assert eng.row_length((2, 131072), 1024) == 0 and eng.row_length((), 1024) == 0
+    tiny = [math.prod(s) for _, s in mg.paramsets.WORKLOADS["minigpt_tiny_cpu"]()]
+    assert eng.default_chunk(tiny) == 2048
+    assert eng.default_chunk([1 << 19, 5]) == 2048            # 256 chunks of 2,048
+    assert eng.default_chunk([(1 << 19) + 1, 5]) == 1024      # 257
+    assert eng.default_chunk([1 << 20] * 2) == 1024           # one tensor of 512 chunks
+    assert eng.default_chunk([1 << 18] * 8) == 2048           # 2,097,152 elements
+    assert eng.default_chunk([1 << 18] * 8 + [1]) == 1024     # one more
+    assert eng.default_chunk([100, 0]) == 1024                # an empty tensor keeps the five kernels
+    gpt2 = [math.prod(s) for _, s in mg.paramsets.WORKLOADS["gpt2_small"]()]
+    assert eng.default_chunk(gpt2) == 1024
