@@ -94,10 +94,12 @@ constexpr int64_t kNormChunk = 131072;
 // step on MI355X, the three-kernel form gains 2-7 us eager and 1-5 us as a
 // replayed graph on sets of up to 2M elements in tensors of at most 256
 // chunks, loses 2-6 us on 4M and 8M elements in 16 tensors, and 3.9 us
-// replayed on one tensor of 1,024 chunks.  Their pass-1 chunks are shorter
-// (4,096-16,384 measured the same).  MGOPT_FOLD=0 in the environment at plan
-// creation keeps the five-kernel form; MGOPT_FOLD=1 takes the three-kernel
-// form beyond the limits too, up to kFoldForcedElems (for measuring them).
+// replayed on one tensor of 1,024 chunks.  Their pass-1 chunks are shorter:
+// replayed steps on 0.8M, 1M and 2M elements measured 16,384 the fastest or
+// tied (4,096 2-5 us slower, 32,768 up to 0.8 us, 65,536 1.4-2.8 us).
+// MGOPT_FOLD=0 in the environment at plan creation keeps the five-kernel
+// form; MGOPT_FOLD=1 takes the three-kernel form beyond the limits too, up to
+// kFoldForcedElems (for measuring them).
 // (Folding only the finalize into a pass 1 of one round of work-groups,
 // GPT-2-small's 950, measured 0.567 ms per step both ways: the ticket each
 // work-group waits for costs what the saved launch gains.)
