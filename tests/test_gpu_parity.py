@@ -9,14 +9,12 @@ norm <= 1e-5 relative.
 
 from __future__ import annotations
 
-import math
-
 import numpy as np
 import pytest
 import torch
 
 from oracle import oracle as O
-from tests._compare import RTOL_NORM, RTOL_STATE, exact_fraction, maxrel, rel
+from tests._compare import RTOL_STATE, maxrel, rel
 from tests._gpu_harness import Case, Pair, check_pair, log, mg, syn
 
 pytestmark = pytest.mark.gpu
