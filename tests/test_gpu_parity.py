@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests._compare import RTOL_STATE, maxrel, rel
+from tests._compare import RTOL_STATE, maxrel
 from tests._gpu_harness import Case, Pair, check_pair, log, mg, syn
 
 pytestmark = pytest.mark.gpu
