@@ -166,6 +166,29 @@ def test_gpt_1p3b_full_size_bf16_master():
     _check_full(pair, "gpt_1p3b", 100)
 
 
+def test_gpt_1p3b_full_size_fp32_params_with_scaler():
+    """The class the reference's loop steps on a GPU (train.py:359-370: fp32
+    parameters and gradients, a GradScaler for fp16 autocast, clip 1.0) at
+    the 1.3B GPT's full size: 1,313,722,368 fp32 params, heavy-tailed grads
+    (clipping every step), growth interval 5, 20 steps with an inf at step 4
+    (a skipped step over the whole set).  Every norm checked against the
+    device fp64 total, three also by the host rebuild; the token embedding,
+    the last matrix and every no-decay tensor tracked from step 1, the other
+    matrices rotated, so every tensor is value-checked."""
+    shapes = mg.paramsets.WORKLOADS["gpt_1p3b"]()
+    decay_n = sum(1 for _, s in shapes if len(s) >= 2)
+    subset = [0, decay_n - 1] + list(range(decay_n, len(shapes)))
+    log("case: gpt_1p3b full size, fp32 params and grads, scaler, 20 steps, inf at step 4")
+    pair = Pair(Case(shapes=shapes, param_dtype="f32", grad_dtype="f32", steps=20, sigma=1e-3, tail=(1000, 100.0),
+                     scaler=dict(init_scale=65536.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=5),
+                     inject={4: [(3, 77, float("inf"))]}, subset=subset, host_grads=True, rotate=True,
+                     verify_norm={1, 4, 20}))
+    _run_full(pair, "gpt_1p3b fp32", check_at={1, 10, 20}, skip_step=4)
+    assert [s + 1 for s, o in enumerate(pair.outs) if o["skipped"]] == [4]
+    assert pair.outs[-1]["scale"] == 65536.0 / 2 * 2 ** 3
+    _check_full(pair, "gpt_1p3b fp32", 19)
+
+
 def test_qwen3_8b_full_size():
     """Qwen3-8B-shaped set, 8,190,735,360 params (131 GB resident): bf16 params
     and grads, fp32 master/m/v, GradScaler, clip 1.0; 100 steps with +inf at
