@@ -3,9 +3,10 @@
 from __future__ import annotations
 
 import ctypes
-import math
 import importlib
+import math
 import re
+import subprocess
 from pathlib import Path
 
 import pytest
@@ -114,6 +115,33 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert getattr(lib, name) is not None
     assert lib.mgopt_version().decode().startswith("mgopt")
+
+
+def test_header_is_c99_and_cxx_and_its_structs_match_the_binding(tmp_path):
+    """include/mgopt.h compiles as strict C99 and as C++17, and the sizes and
+    field offsets of its two structs, as gcc lays them out, are the ones the
+    ctypes binding declares."""
+    native = importlib.import_module("minigpt-train-infra_amd._native")
+    src = tmp_path / "layout.c"
+    fields = [f for f, _ in native.TensorDesc._fields_]
+    gfields = [f for f, _ in native.GroupHparams._fields_]
+    lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "mgopt.h"', "int main(void) {",
+             '    printf("%zu %zu\\n", sizeof(mgopt_tensor_desc), sizeof(mgopt_group_hparams));']
+    lines += [f'    printf("%zu\\n", offsetof(mgopt_tensor_desc, {f}));' for f in fields]
+    lines += [f'    printf("%zu\\n", offsetof(mgopt_group_hparams, {f}));' for f in gfields]
+    lines += ["    return 0;", "}"]
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    inc = str(ROOT / "include")
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", inc, str(src), "-o", str(exe)],
+                   check=True)
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-fsyntax-only", "-x", "c++", "-I", inc,
+                    str(src)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    want = [ctypes.sizeof(native.TensorDesc), ctypes.sizeof(native.GroupHparams)]
+    want += [getattr(native.TensorDesc, f).offset for f in fields]
+    want += [getattr(native.GroupHparams, f).offset for f in gfields]
+    assert got == want
 
 
 def test_c_abi_rejects_bad_arguments_before_touching_the_gpu():
